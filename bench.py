@@ -1,0 +1,301 @@
+"""Benchmark of the Llama-3 inference attention path on one MI355X.
+
+Default workload: paged GQA flash-decode at Llama-3-8B
+shape — 64 sequences, 32 q / 8 kv heads, head_dim 128, bf16, contexts
+~U[512, 8192] (seed 0), 64-token pages in a seeded random permutation. One
+step = one paged_decode_attention call (split-K kernel + merge) over all 64
+sequences, inputs resident in HBM. `value` = algorithmic bytes / step time.
+
+Other workloads (--workload): decode70b (config 5), prefill (config 3,
+TFLOP/s), model8b (config 4, tok/s of a full 8B decode step).
+
+Prints one JSON line with the driver's fields plus `roofline` (the dominant
+kernel against MI355X peaks) and `cpu_baseline` (the CPU oracle on the host
+cores, bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "llm-cuda_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "paged flash-decode GB/s (% HBM peak); prefill attn TFLOPS; decode tok/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# Workload construction
+# ---------------------------------------------------------------------------
+def build_paged(lens, Hq, Hkv, D, P, seed, device):
+    """Pools of exactly sum(ceil(len/P)) pages, block table = seeded permutation
+    split in sequence order, padded with -1 (BASELINE config 2/5 construction)."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    npages = [math.ceil(n / P) for n in lens]
+    N = sum(npages)
+    perm = torch.randperm(N, generator=g).to(torch.int32)
+    bt = torch.full((len(lens), max(npages)), -1, dtype=torch.int32)
+    o = 0
+    for b, n in enumerate(npages):
+        bt[b, :n] = perm[o:o + n]
+        o += n
+    gd = torch.Generator(device=device).manual_seed(seed)
+    kp = torch.randn(N, Hkv, P, D, generator=gd, device=device, dtype=torch.bfloat16)
+    vp = torch.randn(N, Hkv, P, D, generator=gd, device=device, dtype=torch.bfloat16)
+    q = torch.randn(len(lens), Hq, 1, D, generator=gd, device=device, dtype=torch.bfloat16)
+    return q, kp, vp, bt.to(device), torch.tensor(lens, dtype=torch.int32, device=device), bt
+
+
+def decode_bytes(lens, B, Hq, Hkv, D, P):
+    """Algorithmic HBM bytes of one decode call: K and V of every live token,
+    Q, O, lse, the live block-table entries and seq_lens."""
+    kv = sum(lens) * Hkv * D * 2 * 2
+    return kv + B * Hq * D * 2 * 2 + B * Hq * 4 + sum(math.ceil(n / P) for n in lens) * 4 + B * 4
+
+
+def time_steps(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return start.elapsed_time(end) / steps, wall
+
+
+def cpu_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def timed_cpu(fn, budget_s=30.0):
+    """One warm-up, then the median of up to 3 runs within the budget."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    reps = 3 if 4 * first < budget_s else 1
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+def run_decode(args, shape):
+    import torch
+
+    from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
+
+    dev = torch.device("cuda", 0)
+    B, Hq, Hkv, D, P = shape["B"], shape["Hq"], shape["Hkv"], shape["D"], shape["P"]
+    lens = shape["lens"]
+    q, kp, vp, bt, sl, bt_host = build_paged(lens, Hq, Hkv, D, P, shape["seed"], dev)
+    torch.cuda.synchronize()
+    kw = {}
+    if args.split_tokens:
+        kw["split_tokens"] = args.split_tokens
+
+    def step():
+        return paged_decode_attention(q, kp, vp, bt, sl, return_lse=True, **kw)
+
+    ms, wall = time_steps(step, args.steps, args.warmup)
+    nbytes = decode_bytes(lens, B, Hq, Hkv, D, P)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"{shape['name']}: {ms * 1e3:.1f} us/step (host wall {wall * 1e3:.1f} us), "
+        f"{nbytes / 1e9:.4f} GB -> {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 5),
+        "dtype": "bf16",
+        "config": {
+            "workload": shape["workload"],
+            "batch": B, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D, "page_size": P,
+            "context_tokens": sum(lens), "context_min": min(lens), "context_max": max(lens),
+            "page_table": "seeded random permutation",
+            "algorithmic_bytes_per_step": nbytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode_mfma_kernel + decode_merge_kernel (one decode call)",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        from oracle.decode import paged_decode
+
+        torch.set_num_threads(cpu_threads())
+        ns = min(len(lens), shape.get("cpu_sample", 8))
+        qs, kps, vps = q[:ns].cpu(), kp.cpu(), vp.cpu()
+        bts, sls = bt_host[:ns], lens[:ns]
+        secs = timed_cpu(lambda: paged_decode(qs, kps, vps, bts, sls))
+        sbytes = decode_bytes(sls, ns, Hq, Hkv, D, P)
+        cpu_gbs = sbytes / secs / 1e9
+        log(f"cpu oracle: {ns} sequences in {secs:.2f} s -> {cpu_gbs:.2f} GB/s "
+            f"({torch.get_num_threads()} threads)")
+        result["cpu_baseline"] = {
+            "value": round(cpu_gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"first {ns} of {len(lens)} sequences ({sum(sls)} tokens), torch fp32 "
+                      f"gather + per-(b, kv head) matmul/softmax (oracle.decode.paged_decode), "
+                      f"median of runs after one warm-up: {secs:.3f} s",
+        }
+    return result
+
+
+def run_prefill(args):
+    import torch
+
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+    from llm_cuda.models.llama3.rotary import apply_rotary, build_rope_cache
+
+    dev = torch.device("cuda", 0)
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, Hq, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    cos, sin = build_rope_cache(S, D, 500000.0, dev, torch.bfloat16)
+    q, k = apply_rotary(q, k, cos, sin)
+
+    def step():
+        return triton_fused_causal_attention(q, k, v, return_lse=True)
+
+    ms, wall = time_steps(step, args.steps, args.warmup)
+    flops = 2 * B * Hq * D * S * (S + 1)
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"prefill: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s "
+        f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 dense peak)")
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 5),
+        "dtype": "bf16",
+        "config": {"workload": "causal prefill attention, Llama-3-8B shape (BASELINE config 3)",
+                   "batch": B, "seq_len": S, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
+                   "rope_theta": 500000.0, "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "kernel": "prefill attention", "achieved": round(tflops, 2),
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        from oracle.attention import causal_attention
+
+        torch.set_num_threads(cpu_threads())
+        # one batch element, one kv-head group (4 q heads) = 1/32 of the work
+        qs, ks, vs = q[:1, :4].cpu(), k[:1, :1].cpu(), v[:1, :1].cpu()
+        secs = timed_cpu(lambda: causal_attention(qs, ks, vs), budget_s=40.0)
+        sflops = 2 * 1 * 4 * D * S * (S + 1)
+        result["cpu_baseline"] = {
+            "value": round(sflops / secs / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"batch 0, q heads 0-3 / kv head 0 (1/32 of the step), torch fp32 "
+                      f"oracle.attention.causal_attention: {secs:.3f} s"}
+    return result
+
+
+def run_model(args):
+    raise NotImplementedError("model8b workload not implemented yet")
+
+
+def decode8b_shape():
+    import torch
+
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 8193, (64,), generator=g).tolist()
+    return {"name": "decode8b", "B": 64, "Hq": 32, "Hkv": 8, "D": 128, "P": 64, "lens": lens,
+            "seed": 0, "cpu_sample": 8,
+            "workload": "paged GQA flash-decode, Llama-3-8B shape (BASELINE config 2)"}
+
+
+def decode70b_shape():
+    return {"name": "decode70b", "B": 8, "Hq": 64, "Hkv": 8, "D": 128, "P": 64,
+            "lens": [32768] * 8, "seed": 0, "cpu_sample": 1,
+            "workload": "long-context paged decode, Llama-3-70B attention shape (BASELINE config 5)"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default="decode8b",
+                        choices=["decode8b", "decode70b", "prefill", "model8b"])
+    parser.add_argument("--split-tokens", type=int, default=None)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
+              "the multi-GPU sharding is described in DESIGN.md and not implemented.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU available", file=sys.stderr)
+        return 1
+    from llm_cuda import _native
+
+    _native.load()
+    log(f"device {torch.cuda.get_device_name(0)}, workload {args.workload}, "
+        f"steps {args.steps}, warmup {args.warmup}")
+    if args.workload == "decode8b":
+        res = run_decode(args, decode8b_shape())
+    elif args.workload == "decode70b":
+        res = run_decode(args, decode70b_shape())
+    elif args.workload == "prefill":
+        res = run_prefill(args)
+    else:
+        res = run_model(args)
+    line = {
+        "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": res["dtype"], "data": "synthetic (seeded N(0,1) bf16 inputs)",
+        "config": res["config"], "roofline": res["roofline"],
+    }
+    if "cpu_baseline" in res:
+        line["cpu_baseline"] = res["cpu_baseline"]
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,166 @@
+/*
+ * lcuda.h — C ABI of liblcuda_hip.so, the gfx950 (MI355X) kernels behind the
+ * Llama-3 inference attention path of llm_cuda.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers owned by the caller. The library never
+ *     allocates or frees device memory and keeps no device state.
+ *   - Sizes and strides are int64 counts of ELEMENTS (not bytes). The last
+ *     (head_dim / hidden) dimension must have stride 1.
+ *   - `dtype` is one of LC_DTYPE_*; all inputs and outputs of one call share it
+ *     unless a parameter says otherwise. Arithmetic is fp32 throughout.
+ *   - `stream` is a hipStream_t (the caller's current stream); 0 = null stream.
+ *     Launches are asynchronous; no entry point synchronises.
+ *   - Return value: LC_OK (0) on success, a negative LC_E* code when the
+ *     arguments are rejected before any launch, or a positive hipError_t when
+ *     the launch itself failed. lc_last_error() then holds a message
+ *     (thread-local, valid until the next call on the same thread).
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to calvin-fei/llm-cuda, src/llm_cuda/...).
+ */
+#ifndef LCUDA_H_
+#define LCUDA_H_
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define LC_API __attribute__((visibility("default")))
+#else
+#define LC_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LC_DTYPE_F32 = 0,
+  LC_DTYPE_F16 = 1,
+  LC_DTYPE_BF16 = 2,
+};
+
+enum {
+  LC_OK = 0,
+  LC_EINVAL = -1,       /* bad argument (shape, stride, dtype, null pointer) */
+  LC_EUNSUPPORTED = -2, /* valid request this build does not implement       */
+  LC_EWORKSPACE = -3,   /* caller-provided workspace too small               */
+};
+
+/* Library identity. Replaces the extension self-check of
+ * runners/build_cuda_extension.py:1-34 (which printed exported symbols). */
+LC_API int lc_version(void);
+LC_API const char* lc_last_error(void);
+
+/* RMSNorm forward: y[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * w.
+ * Replaces kernels/cuda/csrc/rmsnorm_extension.cpp:9-23 (rms_norm_forward),
+ * kernels/cuda/csrc/rmsnorm_kernel.cu:7-78 and kernels/triton/rmsnorm.py:13-75.
+ * x, y: [rows, hidden] with row strides; w: [hidden] contiguous, of dtype
+ * w_dtype (the reference requires w_dtype == dtype; fp32 weights are also
+ * accepted here). Any hidden size (the Triton path stopped at 4096). */
+LC_API int lc_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
+                   int64_t x_row_stride, int64_t y_row_stride, float eps, int dtype,
+                   int w_dtype, void* stream);
+
+/* SwiGLU forward: out = silu(gate) * up = gate * sigmoid(gate) * up (fp32 math).
+ * Replaces csrc/rmsnorm_extension.cpp:25-40 (swiglu_forward),
+ * csrc/swiglu_kernel.cu:7-57 and kernels/triton/swiglu.py:15-42,91-145.
+ * gate, up, out: [rows, cols] with row strides; any cols. */
+LC_API int lc_swiglu_fwd(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
+                  int64_t gate_row_stride, int64_t up_row_stride, int64_t out_row_stride,
+                  int dtype, void* stream);
+
+/* RoPE forward on one or two tensors in one launch (Q and K of a layer).
+ * out[.., d]      = x[.., d]      * cos[s, d]      - x[.., d+D/2] * sin[s, d]
+ * out[.., d+D/2]  = x[.., d+D/2]  * cos[s, d+D/2]  + x[.., d]     * sin[s, d+D/2]
+ * for d < D/2, i.e. x*cos + rotate_half(x)*sin with the FULL-width tables.
+ * Replaces kernels/triton/rope.py:37-125,156-222 and the fallback of
+ * models/llama3/rotary.py:81-109.
+ * x{1,2}: [B, H{1,2}, S, D] with strides x*_strides[4] (any layout, e.g. the
+ * transposed projection views); out{1,2}: [B, H, S, D] with out*_strides[4]
+ * (may alias x in place). cos, sin: [S, D] with row strides cs_stride_s /
+ * sin_stride_s. Pass x2 = out2 = NULL, h2 = 0 for a single tensor. D even. */
+LC_API int lc_rope_fwd(const void* x1, void* out1, int64_t h1, const int64_t* x1_strides,
+                const int64_t* out1_strides, const void* x2, void* out2, int64_t h2,
+                const int64_t* x2_strides, const int64_t* out2_strides, const void* cos,
+                const void* sin, int64_t cos_stride_s, int64_t sin_stride_s, int64_t B,
+                int64_t S, int64_t D, int dtype, void* stream);
+
+/* Causal attention forward with native GQA and logsumexp.
+ * o[b,h,i,:] = sum_j softmax_j(q[b,h,i,:].k[b,h/G,j,:] * scale) v[b,h/G,j,:]
+ * over keys j <= i + q_offset (j < Skv); lse[b,h,i] = natural-log logsumexp of
+ * the scaled, masked scores (fp32, contiguous [B, Hq, Sq]; may be NULL).
+ * Replaces kernels/triton/attention.py:74-178,323-378,501-535 (forward),
+ * csrc/attention_kernel.cu:12-153 and, for q_offset > 0,
+ * models/llama3/attention.py:63-89 (_torch_attention with past_len).
+ * q, o: [B, Hq, Sq, D]; k, v: [B, Hkv, Skv, D]; strides in *_strides[4].
+ * Hq % Hkv == 0. bf16/f16 run on MFMA (D in {64, 128}); other cases run a
+ * generic fp32-FMA kernel (D <= 256). */
+LC_API int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D,
+                        const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
+                        float scale, int dtype, void* stream);
+
+/* Bytes of fp32 workspace lc_paged_decode_fwd needs for these sizes
+ * (partial outputs and logsumexps of every split). */
+LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits);
+
+/* Split-K paged GQA flash-decode: one query token per sequence against the
+ * K/V pages named by the block table, then a cross-split logsumexp merge.
+ * out[b,h,:] = softmax(q[b,h,:].K_b^T * scale) V_b over the seq_lens[b] tokens
+ * of sequence b, where token t lives in page block_table[b, t / page_size],
+ * slot t % page_size. lse[b,h] (fp32, contiguous [B, Hq], may be NULL) is the
+ * natural-log logsumexp of the scaled scores; empty sequences give out = 0,
+ * lse = -inf.
+ * Replaces kernels/triton/decode_attention.py:47-159,204-287 reading the
+ * contiguous copy made by models/llama3/kv_cache.py:65-83 (get_kv): here the
+ * pages are read in place.
+ * q, out: [B, Hq, D] with (batch, head) strides q_sb/q_sh, o_sb/o_sh.
+ * key_pages, value_pages: [num_pages, Hkv, page_size, D] pools with shared
+ *   element strides kv_s_page, kv_s_head, kv_s_tok.
+ * block_table: int32 [B, max_pages_per_seq] (row stride bt_stride);
+ *   entries outside [0, num_pages) are never dereferenced (their tokens are
+ *   skipped). seq_lens: int32 [B], clamped to max_pages_per_seq * page_size.
+ * split_tokens: tokens per split (multiple of 64); max_splits *
+ *   split_tokens must cover the block-table capacity max_pages_per_seq *
+ *   page_size (so no clamped length can need more splits than the grid has).
+ * workspace: >= lc_paged_decode_workspace_bytes(B, Hq, D, max_splits). */
+LC_API int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* key_pages,
+                        const void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
+                        int64_t kv_s_tok, const int32_t* block_table, int64_t bt_stride,
+                        int64_t max_pages_per_seq, int64_t num_pages, const int32_t* seq_lens,
+                        void* out, int64_t o_sb, int64_t o_sh, float* lse, void* workspace,
+                        int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                        int64_t page_size, int64_t split_tokens, int64_t max_splits, float scale,
+                        int dtype, void* stream);
+
+/* Scatter S new tokens per sequence into the page pools through the block
+ * table: pages[bt[b, (p0_b+s)/P], h, (p0_b+s)%P, :] = x[b, h, s, :] with
+ * p0_b = start_pos[b] (int32 [B], device). K and V in one launch.
+ * Replaces the per-token Python copy loop of models/llama3/kv_cache.py:38-63
+ * (PagedKVLayerCache.append). k_new, v_new: [B, Hkv, S, D] with strides
+ * k_strides[4] / v_strides[4]. Tokens whose page entry is outside
+ * [0, num_pages) or whose position is >= max_pages_per_seq * P are dropped. */
+LC_API int lc_paged_kv_append(const void* k_new, const void* v_new, const int64_t* k_strides,
+                       const int64_t* v_strides, void* key_pages, void* value_pages,
+                       int64_t kv_s_page, int64_t kv_s_head, int64_t kv_s_tok,
+                       const int32_t* block_table, int64_t bt_stride, int64_t max_pages_per_seq,
+                       int64_t num_pages, const int32_t* start_pos, int64_t B, int64_t Hkv,
+                       int64_t S, int64_t D, int64_t page_size, int dtype, void* stream);
+
+/* Gather the first L tokens of every sequence into contiguous
+ * k_out, v_out [B, Hkv, L, D] (bit-exact copy through the block table).
+ * Replaces models/llama3/kv_cache.py:65-83 (PagedKVLayerCache.get_kv).
+ * Tokens whose page entry is outside [0, num_pages) are written as zero. */
+LC_API int lc_paged_kv_gather(const void* key_pages, const void* value_pages, int64_t kv_s_page,
+                       int64_t kv_s_head, int64_t kv_s_tok, const int32_t* block_table,
+                       int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
+                       void* k_out, void* v_out, int64_t B, int64_t Hkv, int64_t L, int64_t D,
+                       int64_t page_size, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LCUDA_H_ */

@@ -1,0 +1,417 @@
+// Single-pass, HBM-bound kernels of the Llama-3 block: RMSNorm, SwiGLU, RoPE.
+//
+// All three read each input byte once and write each output byte once with
+// 16-byte (dwordx4) lane accesses when the layout allows it, and fall back to
+// element-wise access (VEC = 1) for unaligned or oddly strided views.
+// Arithmetic is fp32; results are rounded once to the storage type.
+#include "lc_common.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// RMSNorm: one workgroup per row. The row is held in registers (ITEMS vectors
+// per lane) so it is read from HBM once; ITEMS == 0 selects a two-pass loop
+// for rows too wide to cache (re-read hits L2).
+// Follows kernels/cuda/csrc/rmsnorm_kernel.cu:26-49: y = (x * inv_rms) * w.
+// ---------------------------------------------------------------------------
+template <typename T, typename W, int VEC, int ITEMS>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x,
+                                                      const W* __restrict__ w,
+                                                      T* __restrict__ y, int hidden,
+                                                      int64_t xs, int64_t ys, float eps) {
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * xs;
+  T* yr = y + row * ys;
+  const int nvec = hidden / VEC;
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+
+  float acc = 0.f;
+  float cache[ITEMS > 0 ? ITEMS : 1][VEC];
+  if constexpr (ITEMS > 0) {
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int vi = tid + it * nthreads;
+      if (vi < nvec) {
+        if constexpr (VEC * sizeof(T) == 16) {
+          Vec16<T> v = lc_load16(xr + (int64_t)vi * VEC);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) cache[it][e] = lc_to_f32(v.v[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) cache[it][e] = lc_to_f32(xr[(int64_t)vi * VEC + e]);
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc = fmaf(cache[it][e], cache[it][e], acc);
+      }
+    }
+  } else {
+    for (int vi = tid; vi < nvec; vi += nthreads) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float f = lc_to_f32(xr[(int64_t)vi * VEC + e]);
+        acc = fmaf(f, f, acc);
+      }
+    }
+  }
+
+  __shared__ float red[4];
+  acc = lc_wave_sum(acc);
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) red[wave] = acc;
+  __syncthreads();
+  float total = 0.f;
+  const int nwaves = nthreads >> 6;
+  for (int i = 0; i < nwaves; ++i) total += red[i];
+  const float inv_rms = rsqrtf(total / static_cast<float>(hidden) + eps);
+
+  if constexpr (ITEMS > 0) {
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int vi = tid + it * nthreads;
+      if (vi < nvec) {
+        Vec16<T> out;
+        T* dst = yr + (int64_t)vi * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float wv = lc_to_f32(w[(int64_t)vi * VEC + e]);
+          const T r = lc_from_f32<T>(cache[it][e] * inv_rms * wv);
+          if constexpr (VEC * sizeof(T) == 16) {
+            out.v[e] = r;
+          } else {
+            dst[e] = r;
+          }
+        }
+        if constexpr (VEC * sizeof(T) == 16) lc_store16(dst, out);
+      }
+    }
+  } else {
+    for (int vi = tid; vi < nvec; vi += nthreads) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t c = (int64_t)vi * VEC + e;
+        yr[c] = lc_from_f32<T>(lc_to_f32(xr[c]) * inv_rms * lc_to_f32(w[c]));
+      }
+    }
+  }
+}
+
+template <typename T, typename W, int VEC>
+int launch_rmsnorm_vec(const T* x, const W* w, T* y, int64_t rows, int64_t hidden, int64_t xs,
+                       int64_t ys, float eps, hipStream_t st) {
+  const int64_t nvec = hidden / VEC;
+  int threads = static_cast<int>(lc_cdiv(nvec, 64) * 64);
+  if (threads > 256) threads = 256;
+  if (threads < 64) threads = 64;
+  const int64_t items = lc_cdiv(nvec, threads);
+  dim3 grid(static_cast<unsigned>(rows));
+  if (items <= 1)
+    rmsnorm_kernel<T, W, VEC, 1><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+  else if (items <= 2)
+    rmsnorm_kernel<T, W, VEC, 2><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+  else if (items <= 4)
+    rmsnorm_kernel<T, W, VEC, 4><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+  else if (items <= 8)
+    rmsnorm_kernel<T, W, VEC, 8><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+  else
+    rmsnorm_kernel<T, W, VEC, 0><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+  return lc_check_launch("lc_rmsnorm_fwd");
+}
+
+template <typename T, typename W>
+int launch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
+                   int64_t xs, int64_t ys, float eps, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  const bool vec_ok = (hidden % V == 0) && (xs % V == 0) && (ys % V == 0) &&
+                      lc_aligned(x, 16) && lc_aligned(y, 16);
+  if (vec_ok)
+    return launch_rmsnorm_vec<T, W, V>(static_cast<const T*>(x), static_cast<const W*>(w),
+                                       static_cast<T*>(y), rows, hidden, xs, ys, eps, st);
+  return launch_rmsnorm_vec<T, W, 1>(static_cast<const T*>(x), static_cast<const W*>(w),
+                                     static_cast<T*>(y), rows, hidden, xs, ys, eps, st);
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU: out = g * sigmoid(g) * u, fp32 math
+// (kernels/triton/swiglu.py:37-42: sig = 1 / (1 + exp(-g)); y = (g * sig) * u).
+// 2-D grid: x over column vectors, y over rows (row loop beyond 65535).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = lc_exp2(-g * kLog2e);
+  const float sig = 1.0f / (1.0f + e);
+  return (g * sig) * u;
+}
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ g,
+                                                     const T* __restrict__ u, T* __restrict__ o,
+                                                     int64_t rows, int64_t cols, int64_t gs,
+                                                     int64_t us, int64_t os) {
+  const int64_t vi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t c0 = vi * VEC;
+  if (c0 >= cols) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const T* gr = g + r * gs + c0;
+    const T* ur = u + r * us + c0;
+    T* orow = o + r * os + c0;
+    if constexpr (VEC * sizeof(T) == 16) {
+      Vec16<T> gv = lc_load16(gr);
+      Vec16<T> uv = lc_load16(ur);
+      Vec16<T> ov;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        ov.v[e] = lc_from_f32<T>(silu_mul(lc_to_f32(gv.v[e]), lc_to_f32(uv.v[e])));
+      lc_store16(orow, ov);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if (c0 + e < cols) orow[e] = lc_from_f32<T>(silu_mul(lc_to_f32(gr[e]), lc_to_f32(ur[e])));
+      }
+    }
+  }
+}
+
+template <typename T>
+int launch_swiglu(const void* g, const void* u, void* o, int64_t rows, int64_t cols, int64_t gs,
+                  int64_t us, int64_t os, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  const bool vec_ok = (cols % V == 0) && (gs % V == 0) && (us % V == 0) && (os % V == 0) &&
+                      lc_aligned(g, 16) && lc_aligned(u, 16) && lc_aligned(o, 16);
+  // Fully contiguous tensors are processed as one long row.
+  if (gs == cols && us == cols && os == cols && rows > 1) {
+    cols = rows * cols;
+    rows = 1;
+    gs = us = os = cols;
+  }
+  const int threads = 256;
+  const int vec = vec_ok ? V : 1;
+  const int64_t nvec = lc_cdiv(cols, vec);
+  const int64_t gx = lc_cdiv(nvec, threads);
+  LC_REQUIRE(gx < (1LL << 31), "lc_swiglu_fwd: too many columns (%lld)", (long long)cols);
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(rows < 65535 ? rows : 65535));
+  if (vec_ok)
+    swiglu_kernel<T, V><<<grid, threads, 0, st>>>(static_cast<const T*>(g),
+                                                  static_cast<const T*>(u), static_cast<T*>(o),
+                                                  rows, cols, gs, us, os);
+  else
+    swiglu_kernel<T, 1><<<grid, threads, 0, st>>>(static_cast<const T*>(g),
+                                                  static_cast<const T*>(u), static_cast<T*>(o),
+                                                  rows, cols, gs, us, os);
+  return lc_check_launch("lc_swiglu_fwd");
+}
+
+// ---------------------------------------------------------------------------
+// RoPE: one lane per VEC consecutive rotation pairs (d, d + D/2) of one
+// (tensor, b, h, s) row; Q and K rows share one grid. Full-width cos/sin rows
+// are read (cos[s, d] and cos[s, d + D/2] separately), so tables that are not
+// built as cat(freqs, freqs) are honoured (models/llama3/rotary.py:81-109
+// semantics, not the half-table shortcut of kernels/triton/rope.py:106-108).
+// ---------------------------------------------------------------------------
+struct RopeTensor {
+  const void* x;
+  void* out;
+  int64_t h;
+  int64_t xs[4];
+  int64_t os[4];
+};
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void rope_kernel(RopeTensor t1, RopeTensor t2,
+                                                   const T* __restrict__ cos,
+                                                   const T* __restrict__ sin, int64_t cs_s,
+                                                   int64_t sn_s, int S, int half,
+                                                   int64_t rows1, int64_t rows_total) {
+  const int chunks = half / VEC;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / chunks;
+  if (row >= rows_total) return;
+  const int d0 = static_cast<int>(gid - row * chunks) * VEC;
+
+  const bool second = row >= rows1;
+  const RopeTensor& t = second ? t2 : t1;
+  const int64_t r = second ? row - rows1 : row;
+  const int s = static_cast<int>(r % S);
+  const int64_t bh = r / S;
+  const int64_t h = bh % t.h;
+  const int64_t b = bh / t.h;
+
+  const T* xp = static_cast<const T*>(t.x) + b * t.xs[0] + h * t.xs[1] + (int64_t)s * t.xs[2];
+  T* op = static_cast<T*>(t.out) + b * t.os[0] + h * t.os[1] + (int64_t)s * t.os[2];
+  const T* cp = cos + (int64_t)s * cs_s;
+  const T* sp = sin + (int64_t)s * sn_s;
+
+  float x1[VEC], x2[VEC], c1[VEC], c2[VEC], s1[VEC], s2[VEC];
+  if constexpr (VEC * sizeof(T) == 16) {
+    Vec16<T> a = lc_load16(xp + d0), bb = lc_load16(xp + d0 + half);
+    Vec16<T> ca = lc_load16(cp + d0), cb = lc_load16(cp + d0 + half);
+    Vec16<T> sa = lc_load16(sp + d0), sb = lc_load16(sp + d0 + half);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      x1[e] = lc_to_f32(a.v[e]);
+      x2[e] = lc_to_f32(bb.v[e]);
+      c1[e] = lc_to_f32(ca.v[e]);
+      c2[e] = lc_to_f32(cb.v[e]);
+      s1[e] = lc_to_f32(sa.v[e]);
+      s2[e] = lc_to_f32(sb.v[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      x1[e] = lc_to_f32(xp[d0 + e]);
+      x2[e] = lc_to_f32(xp[d0 + e + half]);
+      c1[e] = lc_to_f32(cp[d0 + e]);
+      c2[e] = lc_to_f32(cp[d0 + e + half]);
+      s1[e] = lc_to_f32(sp[d0 + e]);
+      s2[e] = lc_to_f32(sp[d0 + e + half]);
+    }
+  }
+  Vec16<T> o1, o2;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    const T lo = lc_from_f32<T>(x1[e] * c1[e] - x2[e] * s1[e]);
+    const T hi = lc_from_f32<T>(x2[e] * c2[e] + x1[e] * s2[e]);
+    if constexpr (VEC * sizeof(T) == 16) {
+      o1.v[e] = lo;
+      o2.v[e] = hi;
+    } else {
+      op[d0 + e] = lo;
+      op[d0 + e + half] = hi;
+    }
+  }
+  if constexpr (VEC * sizeof(T) == 16) {
+    lc_store16(op + d0, o1);
+    lc_store16(op + d0 + half, o2);
+  }
+}
+
+template <typename T>
+int launch_rope(const RopeTensor& t1, const RopeTensor& t2, const void* cos, const void* sin,
+                int64_t cs_s, int64_t sn_s, int64_t B, int64_t S, int64_t D, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  const int64_t half = D / 2;
+  auto tensor_vec_ok = [&](const RopeTensor& t) {
+    if (t.h == 0) return true;
+    for (int i = 0; i < 3; ++i)
+      if (t.xs[i] % V != 0 || t.os[i] % V != 0) return false;
+    return lc_aligned(t.x, 16) && lc_aligned(t.out, 16);
+  };
+  const bool vec_ok = (half % V == 0) && (cs_s % V == 0) && (sn_s % V == 0) &&
+                      lc_aligned(cos, 16) && lc_aligned(sin, 16) && tensor_vec_ok(t1) &&
+                      tensor_vec_ok(t2);
+  const int64_t rows1 = B * t1.h * S;
+  const int64_t rows_total = rows1 + B * t2.h * S;
+  const int vec = vec_ok ? V : 1;
+  const int64_t threads_total = rows_total * (half / vec);
+  const int threads = 256;
+  const int64_t blocks = lc_cdiv(threads_total, threads);
+  LC_REQUIRE(blocks < (1LL << 31), "lc_rope_fwd: problem too large");
+  if (blocks == 0) return LC_OK;
+  if (vec_ok)
+    rope_kernel<T, V><<<(unsigned)blocks, threads, 0, st>>>(
+        t1, t2, static_cast<const T*>(cos), static_cast<const T*>(sin), cs_s, sn_s, (int)S,
+        (int)half, rows1, rows_total);
+  else
+    rope_kernel<T, 1><<<(unsigned)blocks, threads, 0, st>>>(
+        t1, t2, static_cast<const T*>(cos), static_cast<const T*>(sin), cs_s, sn_s, (int)S,
+        (int)half, rows1, rows_total);
+  return lc_check_launch("lc_rope_fwd");
+}
+
+}  // namespace
+
+extern "C" {
+
+int lc_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
+                   int64_t x_row_stride, int64_t y_row_stride, float eps, int dtype, int w_dtype,
+                   void* stream) {
+  LC_REQUIRE(rows >= 0 && hidden > 0, "lc_rmsnorm_fwd: bad shape rows=%lld hidden=%lld",
+             (long long)rows, (long long)hidden);
+  LC_REQUIRE(hidden < (1LL << 31) && rows < (1LL << 31), "lc_rmsnorm_fwd: shape too large");
+  LC_REQUIRE(x && w && y, "lc_rmsnorm_fwd: null pointer");
+  LC_REQUIRE(w_dtype == dtype || w_dtype == LC_DTYPE_F32,
+             "lc_rmsnorm_fwd: weight dtype must equal x dtype or be fp32");
+  if (rows == 0) return LC_OK;
+  hipStream_t st = lc_stream(stream);
+  switch (dtype) {
+    case LC_DTYPE_F32:
+      return launch_rmsnorm<float, float>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps,
+                                          st);
+    case LC_DTYPE_BF16:
+      return w_dtype == LC_DTYPE_F32
+                 ? launch_rmsnorm<bf16_t, float>(x, w, y, rows, hidden, x_row_stride,
+                                                 y_row_stride, eps, st)
+                 : launch_rmsnorm<bf16_t, bf16_t>(x, w, y, rows, hidden, x_row_stride,
+                                                  y_row_stride, eps, st);
+    case LC_DTYPE_F16:
+      return w_dtype == LC_DTYPE_F32
+                 ? launch_rmsnorm<f16_t, float>(x, w, y, rows, hidden, x_row_stride,
+                                                y_row_stride, eps, st)
+                 : launch_rmsnorm<f16_t, f16_t>(x, w, y, rows, hidden, x_row_stride,
+                                                y_row_stride, eps, st);
+    default:
+      return lc_fail(LC_EINVAL, "lc_rmsnorm_fwd: unknown dtype %d", dtype);
+  }
+}
+
+int lc_swiglu_fwd(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
+                  int64_t gate_row_stride, int64_t up_row_stride, int64_t out_row_stride,
+                  int dtype, void* stream) {
+  LC_REQUIRE(rows >= 0 && cols >= 0, "lc_swiglu_fwd: bad shape");
+  LC_REQUIRE(gate && up && out, "lc_swiglu_fwd: null pointer");
+  if (rows == 0 || cols == 0) return LC_OK;
+  hipStream_t st = lc_stream(stream);
+  switch (dtype) {
+    case LC_DTYPE_F32:
+      return launch_swiglu<float>(gate, up, out, rows, cols, gate_row_stride, up_row_stride,
+                                  out_row_stride, st);
+    case LC_DTYPE_BF16:
+      return launch_swiglu<bf16_t>(gate, up, out, rows, cols, gate_row_stride, up_row_stride,
+                                   out_row_stride, st);
+    case LC_DTYPE_F16:
+      return launch_swiglu<f16_t>(gate, up, out, rows, cols, gate_row_stride, up_row_stride,
+                                  out_row_stride, st);
+    default:
+      return lc_fail(LC_EINVAL, "lc_swiglu_fwd: unknown dtype %d", dtype);
+  }
+}
+
+int lc_rope_fwd(const void* x1, void* out1, int64_t h1, const int64_t* x1_strides,
+                const int64_t* out1_strides, const void* x2, void* out2, int64_t h2,
+                const int64_t* x2_strides, const int64_t* out2_strides, const void* cos,
+                const void* sin, int64_t cos_stride_s, int64_t sin_stride_s, int64_t B,
+                int64_t S, int64_t D, int dtype, void* stream) {
+  LC_REQUIRE(D > 0 && D % 2 == 0, "lc_rope_fwd: head_dim must be even and > 0 (got %lld)",
+             (long long)D);
+  LC_REQUIRE(B >= 0 && S >= 0 && h1 >= 0 && h2 >= 0, "lc_rope_fwd: bad shape");
+  LC_REQUIRE(x1 && out1 && x1_strides && out1_strides && cos && sin,
+             "lc_rope_fwd: null pointer");
+  LC_REQUIRE(h2 == 0 || (x2 && out2 && x2_strides && out2_strides),
+             "lc_rope_fwd: second tensor incomplete");
+  LC_REQUIRE(x1_strides[3] == 1 && out1_strides[3] == 1 &&
+                 (h2 == 0 || (x2_strides[3] == 1 && out2_strides[3] == 1)),
+             "lc_rope_fwd: head_dim stride must be 1");
+  // With h2 == 0 the grid covers only the rows of tensor 1, so tensor 2 is
+  // never addressed.
+  RopeTensor t1{x1, out1, h1, {}, {}};
+  RopeTensor t2{x2, out2, h2, {}, {}};
+  for (int i = 0; i < 4; ++i) {
+    t1.xs[i] = x1_strides[i];
+    t1.os[i] = out1_strides[i];
+    t2.xs[i] = h2 ? x2_strides[i] : 0;
+    t2.os[i] = h2 ? out2_strides[i] : 0;
+  }
+  LC_REQUIRE(B * (h1 + h2) * S < (1LL << 40), "lc_rope_fwd: problem too large");
+  hipStream_t st = lc_stream(stream);
+  switch (dtype) {
+    case LC_DTYPE_F32:
+      return launch_rope<float>(t1, t2, cos, sin, cos_stride_s, sin_stride_s, B, S, D, st);
+    case LC_DTYPE_BF16:
+      return launch_rope<bf16_t>(t1, t2, cos, sin, cos_stride_s, sin_stride_s, B, S, D, st);
+    case LC_DTYPE_F16:
+      return launch_rope<f16_t>(t1, t2, cos, sin, cos_stride_s, sin_stride_s, B, S, D, st);
+    default:
+      return lc_fail(LC_EINVAL, "lc_rope_fwd: unknown dtype %d", dtype);
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,341 @@
+"""Tensor-level wrappers over the C ABI (include/lcuda.h).
+
+Every function here validates shapes on the host, allocates outputs and
+workspace through torch's caching allocator on the inputs' device, and
+launches on torch's current stream of that device. Inputs must be ROCm
+device tensors; anything else raises (there is no second implementation).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from llm_cuda import _native as nat
+
+
+def _i64arr(vals):
+    import ctypes
+
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def _stream(dev: torch.device) -> int:
+    return nat.stream_ptr(dev)
+
+
+class _DeviceGuard:
+    """Make `dev` current for the launch if it is not already."""
+
+    def __init__(self, dev: torch.device):
+        self.dev = dev
+        self.prev = None
+
+    def __enter__(self):
+        idx = self.dev.index if self.dev.index is not None else torch.cuda.current_device()
+        cur = torch.cuda.current_device()
+        if cur != idx:
+            self.prev = cur
+            torch.cuda.set_device(idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm  (reference: kernels/triton/rmsnorm.py:46-75, norm.py:22-33)
+# ---------------------------------------------------------------------------
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    dev = nat.require_device(x, weight)
+    if weight.dim() != 1 or weight.shape[0] != x.shape[-1]:
+        raise ValueError(f"weight shape {tuple(weight.shape)} does not match hidden {x.shape[-1]}")
+    hidden = x.shape[-1]
+    x2 = x.reshape(-1, hidden)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    if w.dtype != x.dtype and w.dtype != torch.float32:
+        w = w.to(x.dtype)
+    y = torch.empty((x2.shape[0], hidden), dtype=x.dtype, device=dev)
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_rmsnorm_fwd(
+            x2.data_ptr(), w.data_ptr(), y.data_ptr(), x2.shape[0], hidden, x2.stride(0),
+            y.stride(0), float(eps), nat.lc_dtype(x), nat.lc_dtype(w), _stream(dev))
+    nat.check(rc, "lc_rmsnorm_fwd")
+    return y.view(x.shape)
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU  (reference: kernels/triton/swiglu.py:91-145,199-200)
+# ---------------------------------------------------------------------------
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    if gate.shape != up.shape:
+        raise ValueError("gate and up must have matching shapes")
+    if gate.dtype != up.dtype:
+        raise TypeError("gate and up must have the same dtype")
+    dev = nat.require_device(gate, up)
+    cols = gate.shape[-1] if gate.dim() > 0 else 1
+    g2 = gate.reshape(-1, cols)
+    u2 = up.reshape(-1, cols)
+    if g2.stride(-1) != 1:
+        g2 = g2.contiguous()
+    if u2.stride(-1) != 1:
+        u2 = u2.contiguous()
+    out = torch.empty((g2.shape[0], cols), dtype=gate.dtype, device=dev)
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_swiglu_fwd(
+            g2.data_ptr(), u2.data_ptr(), out.data_ptr(), g2.shape[0], cols, g2.stride(0),
+            u2.stride(0), out.stride(0), nat.lc_dtype(gate), _stream(dev))
+    nat.check(rc, "lc_swiglu_fwd")
+    return out.view(gate.shape)
+
+
+# ---------------------------------------------------------------------------
+# RoPE  (reference: kernels/triton/rope.py:156-222, rotary.py:81-109)
+# ---------------------------------------------------------------------------
+def _check_rope_operand(x: torch.Tensor, cos: torch.Tensor, name: str) -> None:
+    if x.dim() != 4:
+        raise ValueError(f"{name} must be [batch, heads, seq, head_dim], got {tuple(x.shape)}")
+    if x.shape[-1] % 2 != 0:
+        raise ValueError(f"{name} head_dim must be even")
+    if tuple(cos.shape) != (x.shape[-2], x.shape[-1]):
+        raise ValueError(
+            f"cos/sin shape {tuple(cos.shape)} must be [seq, head_dim] = "
+            f"{(x.shape[-2], x.shape[-1])}")
+    if x.dtype != cos.dtype:
+        raise TypeError(f"{name} dtype {x.dtype} differs from cos/sin dtype {cos.dtype}")
+
+
+def rope(x1: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+         x2: torch.Tensor | None = None):
+    """Rotate x1 (and x2) in one launch; returns contiguous new tensors."""
+    if cos.shape != sin.shape or cos.dtype != sin.dtype:
+        raise ValueError("cos and sin must have the same shape and dtype")
+    _check_rope_operand(x1, cos, "x")
+    if x2 is not None:
+        _check_rope_operand(x2, cos, "k")
+        if x2.shape[0] != x1.shape[0] or x2.shape[2:] != x1.shape[2:]:
+            raise ValueError("q and k must share batch, seq and head_dim")
+    dev = nat.require_device(x1, cos, sin, x2)
+    if x1.stride(-1) != 1:
+        x1 = x1.contiguous()
+    if x2 is not None and x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if cos.stride(-1) != 1:
+        cos = cos.contiguous()
+    if sin.stride(-1) != 1:
+        sin = sin.contiguous()
+    B, H1, S, D = x1.shape
+    o1 = torch.empty((B, H1, S, D), dtype=x1.dtype, device=dev)
+    o2 = None if x2 is None else torch.empty(tuple(x2.shape), dtype=x2.dtype, device=dev)
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_rope_fwd(
+            x1.data_ptr(), o1.data_ptr(), H1, _i64arr(x1.stride()), _i64arr(o1.stride()),
+            None if x2 is None else x2.data_ptr(), None if o2 is None else o2.data_ptr(),
+            0 if x2 is None else x2.shape[1],
+            None if x2 is None else _i64arr(x2.stride()),
+            None if o2 is None else _i64arr(o2.stride()),
+            cos.data_ptr(), sin.data_ptr(), cos.stride(0), sin.stride(0), B, S, D,
+            nat.lc_dtype(x1), _stream(dev))
+    nat.check(rc, "lc_rope_fwd")
+    return o1, o2
+
+
+# ---------------------------------------------------------------------------
+# Prefill attention  (reference: kernels/triton/attention.py:323-378,501-535)
+# ---------------------------------------------------------------------------
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offset: int = 0,
+                      scale: float | None = None, return_lse: bool = False):
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [batch, heads, seq, head_dim]")
+    if k.shape != v.shape:
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} shapes differ")
+    B, Hq, Sq, D = q.shape
+    if k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} are incompatible")
+    Hkv, Skv = k.shape[1], k.shape[2]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"n_heads ({Hq}) must be a multiple of n_kv_heads ({Hkv})")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k, v must share a dtype")
+    dev = nat.require_device(q, k, v)
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=dev) if return_lse else None
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_prefill_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            None if lse is None else lse.data_ptr(), B, Hq, Hkv, Sq, Skv, D,
+            _i64arr(q.stride()), _i64arr(k.stride()), _i64arr(v.stride()), _i64arr(out.stride()),
+            int(q_offset), float(scale), nat.lc_dtype(q), _stream(dev))
+    nat.check(rc, "lc_prefill_attn_fwd")
+    return (out, lse) if return_lse else out
+
+
+# ---------------------------------------------------------------------------
+# Paged decode  (reference: kernels/triton/decode_attention.py:204-287 over
+# models/llama3/kv_cache.py:65-83)
+# ---------------------------------------------------------------------------
+def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens: int) -> int:
+    """Tokens per split-K wave.
+
+    A split's partial output costs 2 * G * D * 4 bytes of workspace traffic
+    against split * D * 4 bytes of K/V, so splits of ~64*G tokens keep that
+    overhead near 3%; smaller splits are used only when the grid would
+    otherwise leave the 256 CUs (2 resident waves per SIMD) idle.
+    """
+    split = 64
+    while split < 64 * max(1, group) and split < 1024:
+        split *= 2
+    units = batch * n_kv_heads * ((group + 15) // 16)
+    while split > 64 and units * ((capacity_tokens + split - 1) // split) < 2048:
+        split //= 2
+    return split
+
+
+def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
+                 block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None = None,
+                 return_lse: bool = False, split_tokens: int | None = None,
+                 workspace: torch.Tensor | None = None):
+    """One-token GQA attention per sequence over a paged K/V pool.
+
+    q: [B, Hq, 1, D] or [B, Hq, D]; key_pages, value_pages: [N, Hkv, P, D];
+    block_table: int32 [B, max_pages]; seq_lens: int32 [B]. Returns out with
+    q's shape (and lse [B, Hq] fp32 if return_lse).
+    """
+    squeeze = q.dim() == 3
+    q4 = q.unsqueeze(2) if squeeze else q
+    if q4.dim() != 4 or q4.shape[2] != 1:
+        raise ValueError(f"q must be [batch, heads, 1, head_dim], got {tuple(q.shape)}")
+    if key_pages.dim() != 4 or key_pages.shape != value_pages.shape:
+        raise ValueError("key_pages and value_pages must both be [num_pages, kv_heads, page, dim]")
+    if key_pages.stride() != value_pages.stride():
+        value_pages = value_pages.contiguous()
+        key_pages = key_pages.contiguous()
+    B, Hq, _, D = q4.shape
+    N, Hkv, P, Dk = key_pages.shape
+    if Dk != D:
+        raise ValueError(f"head_dim mismatch: q {D}, pages {Dk}")
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"n_heads ({Hq}) must be a multiple of n_kv_heads ({Hkv})")
+    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise TypeError("block_table and seq_lens must be int32")
+    if block_table.dim() != 2 or block_table.shape[0] != B or seq_lens.shape != (B,):
+        raise ValueError("block_table must be [batch, max_pages] and seq_lens [batch]")
+    if q4.dtype != key_pages.dtype or q4.dtype != value_pages.dtype:
+        raise TypeError("q and the page pools must share a dtype")
+    dev = nat.require_device(q4, key_pages, value_pages, block_table, seq_lens)
+    if q4.stride(-1) != 1:
+        q4 = q4.contiguous()
+    if key_pages.stride(-1) != 1:
+        key_pages = key_pages.contiguous()
+        value_pages = value_pages.contiguous()
+    if block_table.stride(-1) != 1:
+        block_table = block_table.contiguous()
+    if not seq_lens.is_contiguous():
+        seq_lens = seq_lens.contiguous()
+    maxp = block_table.shape[1]
+    capacity = maxp * P
+    G = Hq // Hkv
+    if split_tokens is None:
+        split_tokens = choose_split_tokens(B, Hkv, G, capacity)
+    max_splits = max(1, (capacity + split_tokens - 1) // split_tokens)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    lib = nat.load()
+    need = lib.lc_paged_decode_workspace_bytes(B, Hq, D, max_splits)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+    out = torch.empty((B, Hq, 1, D), dtype=q4.dtype, device=dev)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    with _DeviceGuard(dev):
+        rc = lib.lc_paged_decode_fwd(
+            q4.data_ptr(), q4.stride(0), q4.stride(1), key_pages.data_ptr(),
+            value_pages.data_ptr(), key_pages.stride(0), key_pages.stride(1),
+            key_pages.stride(2), block_table.data_ptr(), block_table.stride(0), maxp, N,
+            seq_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+            None if lse is None else lse.data_ptr(), workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, P, split_tokens,
+            max_splits, float(scale), nat.lc_dtype(q4), _stream(dev))
+    nat.check(rc, "lc_paged_decode_fwd")
+    if squeeze:
+        out = out.squeeze(2)
+    return (out, lse) if return_lse else out
+
+
+# ---------------------------------------------------------------------------
+# Page-pool append / gather  (reference: models/llama3/kv_cache.py:38-83)
+# ---------------------------------------------------------------------------
+def _pool_checks(key_pages, value_pages, block_table):
+    if key_pages.dim() != 4 or key_pages.shape != value_pages.shape:
+        raise ValueError("page pools must both be [num_pages, kv_heads, page, dim]")
+    if key_pages.stride() != value_pages.stride() or key_pages.stride(-1) != 1:
+        raise ValueError("key_pages and value_pages must share a layout with unit dim stride")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2:
+        raise TypeError("block_table must be int32 [batch, max_pages]")
+    if block_table.stride(-1) != 1:
+        raise ValueError("block_table rows must be contiguous")
+
+
+def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, key_pages: torch.Tensor,
+              value_pages: torch.Tensor, block_table: torch.Tensor,
+              start_pos: torch.Tensor) -> None:
+    """Write k_new/v_new [B, Hkv, S, D] at positions start_pos[b] + s."""
+    _pool_checks(key_pages, value_pages, block_table)
+    if k_new.shape != v_new.shape or k_new.dim() != 4:
+        raise ValueError("k_new and v_new must both be [batch, kv_heads, seq, head_dim]")
+    B, Hkv, S, D = k_new.shape
+    N, Hp, P, Dp = key_pages.shape
+    if Hp != Hkv or Dp != D or block_table.shape[0] != B:
+        raise ValueError("new tokens do not match the cache layout")
+    if start_pos.dtype != torch.int32 or start_pos.shape != (B,):
+        raise TypeError("start_pos must be int32 [batch]")
+    if k_new.dtype != key_pages.dtype or v_new.dtype != key_pages.dtype:
+        raise TypeError("new tokens must have the cache dtype")
+    dev = nat.require_device(k_new, v_new, key_pages, value_pages, block_table, start_pos)
+    if k_new.stride(-1) != 1:
+        k_new = k_new.contiguous()
+    if v_new.stride(-1) != 1:
+        v_new = v_new.contiguous()
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_paged_kv_append(
+            k_new.data_ptr(), v_new.data_ptr(), _i64arr(k_new.stride()), _i64arr(v_new.stride()),
+            key_pages.data_ptr(), value_pages.data_ptr(), key_pages.stride(0),
+            key_pages.stride(1), key_pages.stride(2), block_table.data_ptr(),
+            block_table.stride(0), block_table.shape[1], N, start_pos.data_ptr(), B, Hkv, S, D,
+            P, nat.lc_dtype(k_new), _stream(dev))
+    nat.check(rc, "lc_paged_kv_append")
+
+
+def kv_gather(key_pages: torch.Tensor, value_pages: torch.Tensor, block_table: torch.Tensor,
+              length: int):
+    """Contiguous [B, Hkv, length, D] copies of the first `length` tokens."""
+    _pool_checks(key_pages, value_pages, block_table)
+    N, Hkv, P, D = key_pages.shape
+    B = block_table.shape[0]
+    if length > block_table.shape[1] * P:
+        raise ValueError("length exceeds the block-table capacity")
+    dev = nat.require_device(key_pages, value_pages, block_table)
+    k_out = torch.empty((B, Hkv, length, D), dtype=key_pages.dtype, device=dev)
+    v_out = torch.empty_like(k_out)
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_paged_kv_gather(
+            key_pages.data_ptr(), value_pages.data_ptr(), key_pages.stride(0),
+            key_pages.stride(1), key_pages.stride(2), block_table.data_ptr(),
+            block_table.stride(0), block_table.shape[1], N, k_out.data_ptr(), v_out.data_ptr(),
+            B, Hkv, length, D, P, nat.lc_dtype(key_pages), _stream(dev))
+    nat.check(rc, "lc_paged_kv_gather")
+    return k_out, v_out

@@ -1,0 +1,68 @@
+"""Causal prefill attention entry (reference: kernels/triton/attention.py:480-535).
+
+`triton_fused_causal_attention(q, k, v)` computes softmax(q k^T / sqrt(D) +
+causal) v on the lc_prefill_attn_fwd HIP kernel. Differences from the
+reference, all widening the accepted inputs:
+  * GQA is native: k and v may carry fewer heads than q (n_heads a multiple
+    of n_kv_heads); the reference required q.shape == k.shape and its callers
+    materialised the repeated K/V (models/llama3/attention.py:141-142).
+  * `return_lse=True` also returns the fp32 natural-log logsumexp [B, H, S]
+    (the reference kept it internal, attention.py:330-333).
+  * `q_offset` shifts the causal diagonal for queries that continue a cached
+    prefix (key j is visible to query i iff j <= i + q_offset), the masking of
+    models/llama3/attention.py:63-89.
+Additive attention masks are not supported and raise NotImplementedError.
+"""
+from __future__ import annotations
+
+import torch
+
+from llm_cuda.kernels import _ops
+
+
+def _gqa_compatible(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or k.shape != v.shape:
+        return False
+    if q.shape[0] != k.shape[0] or q.shape[3] != k.shape[3]:
+        return False
+    return k.shape[1] > 0 and q.shape[1] % k.shape[1] == 0
+
+
+def can_use_triton_fused_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    attention_mask: torch.Tensor | None = None,
+) -> bool:
+    if attention_mask is not None:
+        return False
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        return False
+    if not _gqa_compatible(q, k, v):
+        return False
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return False
+    if not (q.dtype == k.dtype == v.dtype):
+        return False
+    if q.shape[-1] > 256:
+        return False
+    return True
+
+
+def triton_fused_causal_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    attention_mask: torch.Tensor | None = None,
+    *,
+    return_lse: bool = False,
+    q_offset: int = 0,
+):
+    """Causal attention for q [B, Hq, S, D], k/v [B, Hkv, Skv, D]."""
+    if not _gqa_compatible(q, k, v):
+        raise ValueError(
+            "q, k, v must be [batch, heads, seq, head_dim] with matching batch/head_dim and "
+            "n_heads a multiple of n_kv_heads")
+    if attention_mask is not None:
+        raise NotImplementedError("additive attention masks are not supported by the HIP kernel")
+    return _ops.prefill_attention(q, k, v, q_offset=q_offset, return_lse=return_lse)

@@ -1,0 +1,126 @@
+"""Llama-3 attention (reference: models/llama3/attention.py:1-150).
+
+Same module, parameters and call signature as the reference. The forward pass
+differs only in how the attention itself is computed, all on HIP kernels:
+
+  * RoPE: Q and K rotated in one launch, reading the transposed projection
+    views directly.
+  * Paged cache, one query token (decode): new K/V are scattered into the page
+    pools and the query attends to the pools in place through the block table
+    (split-K flash-decode). The reference instead copied the whole cache into a
+    contiguous tensor every step (kv_cache.py:65-83) and decoded that.
+  * Prompt / multi-token chunk: causal prefill attention with native GQA (no
+    repeated K/V) and the causal diagonal shifted by the cached prefix length,
+    which covers both the reference's fused path (past_len == 0) and its
+    `_torch_attention` path with `past_len` (attention.py:63-89,144-147).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+from llm_cuda.kernels.triton.decode_attention import (
+    paged_decode_attention,
+    triton_decode_attention,
+)
+
+from .config import Llama3Config
+from .kv_cache import PagedKVLayerCache
+from .rotary import apply_rotary, build_inv_freq, build_rope_cache
+
+
+class Llama3Attention(nn.Module):
+    def __init__(self, config: Llama3Config):
+        super().__init__()
+        if config.tensor_parallel_size > 1:
+            raise NotImplementedError("tensor parallelism is not part of this build")
+        self.config = config
+        self.num_heads = config.num_attention_heads
+        self.num_kv_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        self.num_kv_groups = self.num_heads // self.num_kv_heads
+
+        q_size = self.num_heads * self.head_dim
+        kv_size = self.num_kv_heads * self.head_dim
+        self.q_proj = nn.Linear(config.hidden_size, q_size, bias=False)
+        self.k_proj = nn.Linear(config.hidden_size, kv_size, bias=False)
+        self.v_proj = nn.Linear(config.hidden_size, kv_size, bias=False)
+        self.o_proj = nn.Linear(q_size, config.hidden_size, bias=False)
+
+        # Non-persistent buffer, like the reference: it follows the module's
+        # dtype, so a bf16 model builds its RoPE tables from a bf16 inv_freq.
+        inv_freq = build_inv_freq(
+            head_dim=config.head_dim, base=config.rope_theta, device=torch.device("cpu"))
+        self.register_buffer("inv_freq", inv_freq, persistent=False)
+
+    def _shape(self, x: torch.Tensor, heads: int) -> torch.Tensor:
+        bsz, seq_len, _ = x.shape
+        return x.view(bsz, seq_len, heads, self.head_dim).transpose(1, 2)
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        attention_mask: torch.Tensor | None = None,
+        past_key_value: tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None = None,
+        use_cache: bool = False,
+    ) -> tuple[torch.Tensor, tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None]:
+        if attention_mask is not None:
+            raise NotImplementedError(
+                "additive attention masks are not supported by the HIP attention kernels")
+        bsz, seq_len, _ = x.shape
+
+        q = self._shape(self.q_proj(x), self.num_heads)
+        k = self._shape(self.k_proj(x), self.num_kv_heads)
+        v = self._shape(self.v_proj(x), self.num_kv_heads)
+
+        paged = isinstance(past_key_value, PagedKVLayerCache)
+        if paged:
+            past_len = past_key_value.length
+        elif past_key_value is not None:
+            past_len = past_key_value[0].shape[-2]
+        else:
+            past_len = 0
+
+        cos, sin = build_rope_cache(
+            seq_len=seq_len,
+            head_dim=self.head_dim,
+            base=self.config.rope_theta,
+            device=x.device,
+            dtype=x.dtype,
+            position_offset=past_len,
+            inv_freq=self.inv_freq,
+        )
+        q, k = apply_rotary(q, k, cos, sin)
+
+        if paged:
+            cache = past_key_value
+            if use_cache:
+                cache.append(k, v)
+            present = cache if use_cache else None
+            if seq_len == 1:
+                # The reference attends to get_kv(): the cache after the
+                # append (or without the new token when use_cache is False).
+                if cache.length == 0:
+                    raise ValueError("decode step against an empty cache")
+                out = paged_decode_attention(
+                    q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens)
+            elif use_cache and past_len == 0:
+                out = triton_fused_causal_attention(q, k, v)
+            else:
+                k_all, v_all = cache.get_kv()
+                out = triton_fused_causal_attention(q, k_all, v_all, q_offset=past_len)
+        else:
+            if past_key_value is not None:
+                past_k, past_v = past_key_value
+                k = torch.cat([past_k, k], dim=-2)
+                v = torch.cat([past_v, v], dim=-2)
+            present = (k, v) if use_cache else None
+            if seq_len == 1 and past_len > 0:
+                out = triton_decode_attention(q, k, v)
+            else:
+                out = triton_fused_causal_attention(q, k, v, q_offset=past_len)
+
+        out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
+        return self.o_proj(out), present
+

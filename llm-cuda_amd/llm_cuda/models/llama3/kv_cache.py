@@ -1,0 +1,159 @@
+"""Paged KV cache with a real block table (reference: models/llama3/kv_cache.py:1-125).
+
+Layout (unchanged from the reference): per layer, `key_pages` and
+`value_pages` are pools [num_pages, n_kv_heads, page_size, head_dim] in the
+model dtype; token t of a sequence lives in page t // page_size, slot
+t % page_size of that sequence's pages. What changes:
+  * `block_table` (int32 [batch, max_pages]) maps each sequence's logical page
+    to a physical page of the pool. The default table gives sequence b the
+    pages b*max_pages .. (b+1)*max_pages - 1, so for batch 1 logical page i IS
+    physical page i, the reference's identity mapping (kv_cache.py:55-57).
+  * batch > 1 and per-sequence lengths (`seq_lens`, int32 [batch] on the
+    device, mirrored on the host in `lengths`).
+  * `append` is one HIP scatter launch (lc_paged_kv_append) instead of a Python
+    loop of 2*seq slice copies; `get_kv` is one HIP gather (lc_paged_kv_gather)
+    instead of a torch.cat of pages. The decode path does not call get_kv at
+    all: it reads the pools in place (paged_decode_attention).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from llm_cuda.kernels import _ops
+
+
+class PagedKVLayerCache:
+    def __init__(
+        self,
+        num_kv_heads: int,
+        head_dim: int,
+        max_seq_len: int,
+        page_size: int,
+        device: torch.device,
+        dtype: torch.dtype,
+        batch_size: int = 1,
+        block_table: torch.Tensor | None = None,
+        num_pages: int | None = None,
+    ):
+        if page_size <= 0:
+            raise ValueError("page_size must be > 0")
+        if max_seq_len <= 0:
+            raise ValueError("max_seq_len must be > 0")
+        if batch_size <= 0:
+            raise ValueError("batch_size must be > 0")
+
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+        self.page_size = page_size
+        self.batch_size = batch_size
+        self.max_pages = math.ceil(max_seq_len / page_size)
+        device = torch.device(device)
+
+        if block_table is None:
+            pool = batch_size * self.max_pages if num_pages is None else num_pages
+            if pool < batch_size * self.max_pages:
+                raise ValueError("num_pages too small for the default block table")
+            block_table = torch.arange(
+                batch_size * self.max_pages, dtype=torch.int32, device=device
+            ).view(batch_size, self.max_pages)
+        else:
+            if block_table.dtype != torch.int32 or block_table.shape != (batch_size, self.max_pages):
+                raise ValueError(
+                    f"block_table must be int32 [{batch_size}, {self.max_pages}]")
+            block_table = block_table.to(device).contiguous()
+            pool = int(block_table.max().item()) + 1 if num_pages is None else num_pages
+        self.num_pages = pool
+        self.block_table = block_table
+
+        self.key_pages = torch.empty(
+            pool, num_kv_heads, page_size, head_dim, device=device, dtype=dtype)
+        self.value_pages = torch.empty_like(self.key_pages)
+        self.seq_lens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        self.lengths = [0] * batch_size
+
+    @property
+    def length(self) -> int:
+        """Cached tokens per sequence (all sequences advance together in `append`)."""
+        first = self.lengths[0]
+        if any(n != first for n in self.lengths):
+            raise ValueError("sequences have different lengths; use `lengths`")
+        return first
+
+    def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        if k.shape != v.shape:
+            raise ValueError("k and v shapes must match")
+        if k.dim() != 4:
+            raise ValueError("Expected k/v shape [batch, kv_heads, seq, head_dim]")
+        if k.shape[0] != self.batch_size:
+            raise ValueError(
+                f"batch {k.shape[0]} does not match the cache batch size {self.batch_size}")
+        if k.shape[1] != self.num_kv_heads or k.shape[3] != self.head_dim:
+            raise ValueError("k/v shapes do not match cache layout")
+        seq = k.shape[2]
+        if max(self.lengths) + seq > self.max_seq_len:
+            raise ValueError("Appending would exceed max_seq_len")
+        if seq == 0:
+            return
+        _ops.kv_append(k, v, self.key_pages, self.value_pages, self.block_table, self.seq_lens)
+        self.seq_lens.add_(seq)
+        self.lengths = [n + seq for n in self.lengths]
+
+    def get_kv(self) -> tuple[torch.Tensor, torch.Tensor]:
+        length = self.length
+        if length == 0:
+            empty = self.key_pages.new_empty(
+                (self.batch_size, self.num_kv_heads, 0, self.head_dim))
+            return empty, empty
+        return _ops.kv_gather(self.key_pages, self.value_pages, self.block_table, length)
+
+    def clear(self) -> None:
+        self.lengths = [0] * self.batch_size
+        self.seq_lens.zero_()
+
+
+class PagedKVCache:
+    def __init__(self, layer_caches: list[PagedKVLayerCache]):
+        if not layer_caches:
+            raise ValueError("layer_caches must not be empty")
+        self.layer_caches = layer_caches
+
+    @classmethod
+    def create(
+        cls,
+        num_layers: int,
+        num_kv_heads: int,
+        head_dim: int,
+        max_seq_len: int,
+        page_size: int,
+        device: torch.device,
+        dtype: torch.dtype,
+        batch_size: int = 1,
+        block_table: torch.Tensor | None = None,
+        num_pages: int | None = None,
+    ) -> "PagedKVCache":
+        return cls(
+            [
+                PagedKVLayerCache(
+                    num_kv_heads=num_kv_heads,
+                    head_dim=head_dim,
+                    max_seq_len=max_seq_len,
+                    page_size=page_size,
+                    device=device,
+                    dtype=dtype,
+                    batch_size=batch_size,
+                    block_table=block_table,
+                    num_pages=num_pages,
+                )
+                for _ in range(num_layers)
+            ]
+        )
+
+    def get_layer(self, layer_idx: int) -> PagedKVLayerCache:
+        return self.layer_caches[layer_idx]
+
+    def clear(self) -> None:
+        for layer in self.layer_caches:
+            layer.clear()

@@ -1,0 +1,157 @@
+"""Llama-3 decoder stack and causal LM (reference: models/llama3/model.py:1-218).
+
+Module structure, parameter names, initialisation (normal(0, initializer_range)
+for every Linear and Embedding, reference model.py:120-139) and the greedy
+`generate` loop follow the reference. `generate(use_paged_kv=True)` accepts a
+batch of any size (the reference's paged cache was batch-1 only). The loss
+path uses torch's cross entropy (the fused Triton cross entropy of the
+reference is outside the attention path); activation checkpointing is a
+training feature and is not provided.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attention import Llama3Attention
+from .config import Llama3Config
+from .kv_cache import PagedKVCache, PagedKVLayerCache
+from .mlp import Llama3MLP
+from .norm import RMSNorm
+
+
+class Llama3DecoderLayer(nn.Module):
+    def __init__(self, config: Llama3Config):
+        super().__init__()
+        self.input_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
+        self.self_attn = Llama3Attention(config)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
+        self.mlp = Llama3MLP(config)
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        attention_mask: torch.Tensor | None = None,
+        past_key_value: tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None = None,
+        use_cache: bool = False,
+    ) -> tuple[torch.Tensor, tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None]:
+        attn_out, present = self.self_attn(
+            self.input_layernorm(x),
+            attention_mask=attention_mask,
+            past_key_value=past_key_value,
+            use_cache=use_cache,
+        )
+        x = x + attn_out
+        x = x + self.mlp(self.post_attention_layernorm(x))
+        return x, present
+
+
+class Llama3Model(nn.Module):
+    def __init__(self, config: Llama3Config):
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList(
+            [Llama3DecoderLayer(config) for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, config.rms_norm_eps)
+
+    def forward(
+        self,
+        input_ids: torch.Tensor,
+        attention_mask: torch.Tensor | None = None,
+        past_key_values: list[tuple[torch.Tensor, torch.Tensor]] | PagedKVCache | None = None,
+        use_cache: bool = False,
+    ) -> dict:
+        x = self.embed_tokens(input_ids)
+        paged = isinstance(past_key_values, PagedKVCache)
+        presents: list[tuple[torch.Tensor, torch.Tensor]] = []
+        for idx, layer in enumerate(self.layers):
+            if paged:
+                layer_past = past_key_values.get_layer(idx)
+            else:
+                layer_past = None if past_key_values is None else past_key_values[idx]
+            x, present = layer(
+                x, attention_mask=attention_mask, past_key_value=layer_past, use_cache=use_cache)
+            if use_cache and not paged and present is not None:
+                presents.append(present)
+        x = self.norm(x)
+        if paged:
+            next_cache = past_key_values if use_cache else None
+        else:
+            next_cache = presents if use_cache else None
+        return {"hidden_states": x, "past_key_values": next_cache}
+
+
+class Llama3ForCausalLM(nn.Module):
+    def __init__(self, config: Llama3Config):
+        super().__init__()
+        self.config = config
+        self.model = Llama3Model(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+        self.apply(self._init_weights)
+
+    def _init_weights(self, module: nn.Module) -> None:
+        if isinstance(module, nn.Linear):
+            nn.init.normal_(module.weight, mean=0.0, std=self.config.initializer_range)
+            if module.bias is not None:
+                nn.init.zeros_(module.bias)
+        elif isinstance(module, nn.Embedding):
+            nn.init.normal_(module.weight, mean=0.0, std=self.config.initializer_range)
+
+    def forward(
+        self,
+        input_ids: torch.Tensor,
+        attention_mask: torch.Tensor | None = None,
+        labels: torch.Tensor | None = None,
+        past_key_values: list[tuple[torch.Tensor, torch.Tensor]] | PagedKVCache | None = None,
+        use_cache: bool = False,
+    ) -> dict:
+        model_out = self.model(
+            input_ids,
+            attention_mask=attention_mask,
+            past_key_values=past_key_values,
+            use_cache=use_cache,
+        )
+        logits = self.lm_head(model_out["hidden_states"])
+        loss = None
+        if labels is not None:
+            shift_logits = logits[:, :-1, :].reshape(-1, self.config.vocab_size)
+            shift_labels = labels[:, 1:].reshape(-1)
+            loss = F.cross_entropy(shift_logits.float(), shift_labels, ignore_index=-100)
+        return {"logits": logits, "loss": loss, "past_key_values": model_out["past_key_values"]}
+
+    @torch.no_grad()
+    def generate(
+        self,
+        input_ids: torch.Tensor,
+        max_new_tokens: int = 16,
+        use_paged_kv: bool = False,
+        page_size: int = 64,
+    ) -> torch.Tensor:
+        """Greedy decoding; returns prompt + max_new_tokens ids."""
+        self.eval()
+        generated = input_ids
+        if use_paged_kv:
+            past_key_values = PagedKVCache.create(
+                num_layers=self.config.num_hidden_layers,
+                num_kv_heads=self.config.num_key_value_heads,
+                head_dim=self.config.head_dim,
+                max_seq_len=input_ids.shape[1] + max_new_tokens,
+                page_size=page_size,
+                device=input_ids.device,
+                dtype=self.model.embed_tokens.weight.dtype,
+                batch_size=input_ids.shape[0],
+            )
+        else:
+            past_key_values = None
+        cur_input = input_ids
+        for _ in range(max_new_tokens):
+            out = self.forward(input_ids=cur_input, past_key_values=past_key_values, use_cache=True)
+            past_key_values = out["past_key_values"]
+            next_token = torch.argmax(out["logits"][:, -1, :], dim=-1, keepdim=True)
+            generated = torch.cat([generated, next_token], dim=1)
+            cur_input = next_token
+        return generated

@@ -1,0 +1,43 @@
+"""Causal attention oracle (fp32 on the host). TEST INFRASTRUCTURE ONLY.
+
+Follows the reference's torch fallback kernels/triton/attention.py:457-477
+(scores = q k^T * scale, triu(-inf, 1) causal mask, softmax, probs @ v) and,
+for a cached prefix, models/llama3/attention.py:63-89 (key j visible to query
+i iff j <= past_len + i). GQA is expressed as the reference's repeat-KV
+(models/llama3/attention.py:56-61): query head h reads kv head h // G.
+Returns the output and the natural-log logsumexp of the masked scores.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+
+def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offset: int = 0,
+                     scale: float | None = None, row_chunk: int = 1024):
+    """q [B, Hq, Sq, D]; k, v [B, Hkv, Skv, D] -> (o fp32 [B, Hq, Sq, D], lse fp32 [B, Hq, Sq])."""
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    out = torch.zeros((B, Hq, Sq, D), dtype=torch.float32)
+    lse = torch.full((B, Hq, Sq), float("-inf"), dtype=torch.float32)
+    key_pos = torch.arange(Skv).view(1, 1, Skv)
+    for b in range(B):
+        for kvh in range(Hkv):
+            kk = k[b, kvh].float()
+            vv = v[b, kvh].float()
+            qg = q[b, kvh * G:(kvh + 1) * G].float()  # [G, Sq, D]
+            for i0 in range(0, Sq, row_chunk):
+                i1 = min(Sq, i0 + row_chunk)
+                s = torch.matmul(qg[:, i0:i1], kk.t()) * scale  # [G, rows, Skv]
+                q_pos = torch.arange(i0, i1).view(1, -1, 1) + q_offset
+                s = s.masked_fill(key_pos > q_pos, float("-inf"))
+                row_lse = torch.logsumexp(s, dim=-1)  # [G, rows]
+                ok = torch.isfinite(row_lse)
+                p = torch.exp(s - torch.where(ok, row_lse, torch.zeros_like(row_lse)).unsqueeze(-1))
+                p = torch.where(ok.unsqueeze(-1), p, torch.zeros_like(p))
+                out[b, kvh * G:(kvh + 1) * G, i0:i1] = torch.matmul(p, vv)
+                lse[b, kvh * G:(kvh + 1) * G, i0:i1] = row_lse
+    return out, lse

@@ -1,0 +1,182 @@
+"""C-ABI boundary and host-side checks that need no GPU.
+
+The library must load, export exactly the entry points include/lcuda.h
+declares, and reject bad arguments before any launch (negative status plus a
+message). The Python entry points must reject host tensors instead of
+computing on the CPU, and keep the reference's predicate/None contracts
+(kernels/cuda/*.py, kernels/triton/*_attention.py, rope.py).
+"""
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "lcuda.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"LC_API\s+[\w\s\*]+?\b(lc_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "lc_paged_decode_fwd" in names and "lc_prefill_attn_fwd" in names
+    assert len(names) >= 10
+
+
+def test_library_exports_every_declared_symbol():
+    from llm_cuda import _native
+
+    lib = _native.load()
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} declared in lcuda.h but not exported"
+    assert set(_declared()) == set(_native.EXPORTS), "ctypes signatures out of sync with lcuda.h"
+    assert lib.lc_version() >= 100
+
+
+def test_exports_nothing_else():
+    import subprocess
+
+    from llm_cuda import _native
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = sorted({ln.split()[-1] for ln in out.splitlines() if " T " in ln})
+    assert exported == _declared()
+
+
+def test_invalid_arguments_rejected_before_launch():
+    from llm_cuda import _native
+
+    lib = _native.load()
+    st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    # null pointers
+    rc = lib.lc_rmsnorm_fwd(None, None, None, 4, 8, 8, 8, 1e-5, 2, 2, None)
+    assert rc == -1 and b"null" in lib.lc_last_error()
+    # Hq not a multiple of Hkv
+    rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 5, 3, 4, 4, 16, st, st, st, st, 0, 1.0, 2,
+                                 None)
+    assert rc == -1 and b"multiple" in lib.lc_last_error()
+    # odd head_dim for RoPE
+    rc = lib.lc_rope_fwd(8, 8, 1, st, st, None, None, 0, None, None, 8, 8, 15, 15, 1, 1, 15, 2,
+                         None)
+    assert rc == -1 and b"even" in lib.lc_last_error()
+    # split does not cover the table capacity
+    rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
+                                 256, 1 << 20, 1, 4, 2, 128, 64, 64, 1, 1.0, 2, None)
+    assert rc == -1 and b"capacity" in lib.lc_last_error()
+    # workspace too small
+    rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
+                                 256, 16, 1, 4, 2, 128, 64, 64, 4, 1.0, 2, None)
+    assert rc == -1 and b"workspace" in lib.lc_last_error()
+    # unknown dtype
+    rc = lib.lc_swiglu_fwd(8, 8, 8, 2, 8, 8, 8, 8, 7, None)
+    assert rc == -1 and b"dtype" in lib.lc_last_error()
+
+
+def test_workspace_size_formula():
+    from llm_cuda import _native
+
+    lib = _native.load()
+    n = 2 * 4 * 3
+    expect = ((n * 128 * 4 + 255) // 256) * 256 + n * 4
+    assert lib.lc_paged_decode_workspace_bytes(2, 4, 128, 3) == expect
+    assert lib.lc_paged_decode_workspace_bytes(-1, 4, 128, 3) == -1
+
+
+def test_host_tensors_rejected():
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+    from llm_cuda.kernels.triton.decode_attention import triton_decode_attention
+    from llm_cuda.kernels.triton.rmsnorm import triton_rms_norm
+    from llm_cuda.kernels.triton.rope import triton_apply_rope
+    from llm_cuda.kernels.triton.swiglu import triton_swiglu
+
+    x = torch.randn(2, 4, 16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        triton_rms_norm(x, torch.ones(16), 1e-5)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        triton_swiglu(x, x)
+    q = torch.randn(1, 2, 8, 16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        triton_fused_causal_attention(q, q, q)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        triton_apply_rope(q, torch.randn(8, 16), torch.randn(8, 16))
+    with pytest.raises(RuntimeError, match="ROCm"):
+        triton_decode_attention(torch.randn(1, 2, 1, 16), q, q)
+
+
+def test_reference_none_contracts_on_host():
+    """kernels/cuda/*.py return None for host tensors (reference test_cuda_extension.py:21-53)."""
+    from llm_cuda.kernels.cuda.attention import cuda_causal_attention_extension
+    from llm_cuda.kernels.cuda.rmsnorm import cuda_extension_status, cuda_rms_norm_extension
+    from llm_cuda.kernels.cuda.swiglu import cuda_swiglu_extension
+
+    x = torch.randn(2, 4, 16)
+    assert cuda_rms_norm_extension(x, torch.randn(16), 1e-5) is None
+    assert cuda_swiglu_extension(x, torch.randn_like(x)) is None
+    q = torch.randn(1, 2, 8, 16)
+    assert cuda_causal_attention_extension(q, q, q) is None
+    status = cuda_extension_status()
+    assert isinstance(status, str) and status
+
+
+def test_predicates_false_on_host():
+    """Guards keep the reference's answers for host tensors and bad shapes
+    (test_triton_decode_attention.py:66-136, test_triton_rope.py:46-93)."""
+    from llm_cuda.kernels.triton.attention import can_use_triton_fused_attention
+    from llm_cuda.kernels.triton.decode_attention import can_use_triton_decode_attention
+    from llm_cuda.kernels.triton.rope import can_use_triton_rope
+
+    q = torch.randn(1, 4, 1, 16, dtype=torch.float16)
+    k = torch.randn(1, 2, 8, 16, dtype=torch.float16)
+    assert can_use_triton_decode_attention(q, k, k) is False
+    assert can_use_triton_fused_attention(q, k, k) is False
+    x = torch.randn(1, 4, 4, 16)
+    assert can_use_triton_rope(x, torch.randn(4, 16), torch.randn(4, 16)) is False
+
+
+def test_config_validation():
+    from llm_cuda.models.llama3.config import Llama3Config
+
+    cfg = Llama3Config(hidden_size=256, num_attention_heads=8, num_key_value_heads=2)
+    assert cfg.head_dim == 32
+    with pytest.raises(ValueError):
+        Llama3Config(hidden_size=250, num_attention_heads=8)
+    with pytest.raises(ValueError):
+        Llama3Config(tensor_parallel_size=0)
+    with pytest.raises(ValueError):
+        Llama3Config(hidden_size=256, num_attention_heads=8, num_key_value_heads=3)
+
+
+def test_kv_cache_argument_checks():
+    from llm_cuda.models.llama3.kv_cache import PagedKVLayerCache
+
+    with pytest.raises(ValueError):
+        PagedKVLayerCache(2, 8, 16, 0, torch.device("cpu"), torch.float32)
+    with pytest.raises(ValueError):
+        PagedKVLayerCache(2, 8, 0, 4, torch.device("cpu"), torch.float32)
+    c = PagedKVLayerCache(2, 8, 10, 4, torch.device("cpu"), torch.float32, batch_size=3)
+    assert c.max_pages == 3 and c.block_table.shape == (3, 3)
+    assert c.block_table.flatten().tolist() == list(range(9))
+    assert c.length == 0
+    with pytest.raises(ValueError, match="batch"):
+        c.append(torch.zeros(1, 2, 1, 8), torch.zeros(1, 2, 1, 8))
+    with pytest.raises(ValueError, match="max_seq_len"):
+        c.append(torch.zeros(3, 2, 11, 8), torch.zeros(3, 2, 11, 8))
+
+
+def test_split_heuristic():
+    from llm_cuda.kernels._ops import choose_split_tokens
+
+    # 8B decode shape: G = 4 -> 256-token splits; 70B long context: G = 8 -> 512.
+    assert choose_split_tokens(64, 8, 4, 8192) == 256
+    assert choose_split_tokens(8, 8, 8, 32768) == 512
+    # tiny batch: splits shrink to keep the grid busy, never below 64.
+    assert choose_split_tokens(1, 2, 4, 128) == 64
+    for args in [(1, 1, 1, 1), (3, 5, 7, 1000), (64, 8, 16, 100000)]:
+        s = choose_split_tokens(*args)
+        assert s % 64 == 0 and 64 <= s <= 1024

@@ -1,0 +1,177 @@
+"""GPU parity: split-K paged flash-decode (MFMA bf16/f16 kernel, generic fp32
+kernel) and the contiguous triton_decode_attention entry vs the oracle.
+
+Cases follow the reference's decode tests (test_triton_decode_attention.py:
+187-302, seed 42: MHA/GQA fp32, fp16, bf16, kv_len 1, long kv 1024, head_dim
+48, batch > 1) and add what paging brings: ragged lengths, random page
+permutations, NaN-poisoned unused slots, invalid table entries, empty
+sequences, page sizes that are not powers of two, split-count invariance, and
+the BASELINE shapes (8B: 32/8 heads, D 128, P 64; 70B: 64/8 heads).
+"""
+import math
+
+import pytest
+import torch
+
+from helpers import ATOL, assert_close, assert_lse_close
+from oracle.decode import decode_attention, paged_decode
+
+pytestmark = pytest.mark.gpu
+
+
+def _contig_case(bsz, n_heads, n_kv_heads, kv_len, head_dim, dtype, device):
+    torch.manual_seed(42)
+    q = torch.randn(bsz, n_heads, 1, head_dim, dtype=dtype, device=device)
+    k = torch.randn(bsz, n_kv_heads, kv_len, head_dim, dtype=dtype, device=device)
+    v = torch.randn(bsz, n_kv_heads, kv_len, head_dim, dtype=dtype, device=device)
+    return q, k, v
+
+
+@pytest.mark.parametrize(
+    "bsz,n_heads,n_kv_heads,kv_len,head_dim,dtype",
+    [
+        (2, 4, 4, 64, 32, torch.float32),     # MHA fp32
+        (2, 8, 4, 64, 32, torch.float32),     # GQA fp32
+        (1, 16, 8, 128, 64, torch.float16),   # GQA fp16
+        (1, 16, 8, 128, 64, torch.bfloat16),  # GQA bf16
+        (1, 4, 2, 1, 16, torch.float32),      # kv_len 1
+        (1, 8, 4, 1024, 64, torch.float32),   # long kv
+        (1, 4, 2, 32, 48, torch.float32),     # head_dim 48
+        (1, 4, 2, 32, 48, torch.bfloat16),    # head_dim 48 on MFMA (padded to 64)
+        (4, 8, 4, 64, 32, torch.float32),     # batch 4
+        (3, 32, 8, 300, 128, torch.bfloat16),  # 8B head layout, odd length
+        (2, 64, 8, 200, 128, torch.bfloat16),  # 70B head layout
+        (2, 40, 2, 77, 128, torch.bfloat16),   # G = 20 > 16: two head groups
+        (2, 8, 8, 129, 256, torch.bfloat16),   # head_dim 256
+    ],
+)
+def test_triton_decode_attention_matches_oracle(cuda, bsz, n_heads, n_kv_heads, kv_len, head_dim,
+                                                dtype):
+    from llm_cuda.kernels.triton.decode_attention import triton_decode_attention
+
+    q, k, v = _contig_case(bsz, n_heads, n_kv_heads, kv_len, head_dim, dtype, cuda)
+    out, lse = triton_decode_attention(q, k, v, return_lse=True)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    ref, ref_lse = decode_attention(q.cpu(), k.cpu(), v.cpu())
+    assert_close(out, ref, ATOL[dtype], "decode out")
+    assert_lse_close(lse, ref_lse)
+
+
+def _paged_case(lens, Hq, Hkv, D, P, dtype, device, seed=0, poison=True, extra_pages=3):
+    g = torch.Generator().manual_seed(seed)
+    pages_per = [max(1, math.ceil(L / P)) for L in lens]
+    maxp = max(pages_per)
+    N = sum(pages_per) + extra_pages
+    perm = torch.randperm(N, generator=g).to(torch.int32)
+    bt = torch.full((len(lens), maxp), -1, dtype=torch.int32)
+    o = 0
+    for b, n in enumerate(pages_per):
+        bt[b, :n] = perm[o:o + n]
+        o += n
+    kp = torch.randn(N, Hkv, P, D, generator=g).to(dtype)
+    vp = torch.randn(N, Hkv, P, D, generator=g).to(dtype)
+    if poison:
+        # NaN in every slot no sequence owns: a read of one shows up as NaN.
+        owned = torch.zeros(N, P, dtype=torch.bool)
+        for b, L in enumerate(lens):
+            for t in range(L):
+                owned[bt[b, t // P], t % P] = True
+        kp[~owned] = float("nan")
+        vp[~owned] = float("nan")
+    q = torch.randn(len(lens), Hq, 1, D, generator=g).to(dtype)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    return q, kp, vp, bt, sl
+
+
+def _run_paged(q, kp, vp, bt, sl, device, **kw):
+    from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
+
+    return paged_decode_attention(q.to(device), kp.to(device), vp.to(device), bt.to(device),
+                                  sl.to(device), return_lse=True, **kw)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("P", [64, 16, 4, 48])
+def test_paged_ragged_random_permutation(cuda, dtype, P):
+    lens = [1, 5, 64, 65, 200, 513, 3]
+    q, kp, vp, bt, sl = _paged_case(lens, 8, 2, 128, P, dtype, cuda, seed=P)
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert_close(out, ref, ATOL[dtype], f"paged P={P}")
+    assert_lse_close(lse, ref_lse)
+
+
+def test_paged_empty_sequence_and_invalid_entries(cuda):
+    lens = [0, 70, 130]
+    q, kp, vp, bt, sl = _paged_case(lens, 4, 1, 64, 64, torch.bfloat16, cuda, seed=3)
+    # an out-of-range entry beyond each sequence's length is never read
+    bt[1, 2:] = 10 ** 6
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert (out[0].float().cpu() == 0).all()
+    assert torch.isinf(lse[0].cpu()).all()
+    assert_close(out[1:], ref[1:], ATOL[torch.bfloat16], "paged invalid")
+    assert_lse_close(lse[1:], ref_lse[1:])
+
+
+def test_paged_invalid_entry_inside_length_is_skipped(cuda):
+    """A bad page id inside the live range is not dereferenced; its tokens drop out."""
+    lens = [192]
+    q, kp, vp, bt, sl = _paged_case(lens, 4, 2, 64, 64, torch.bfloat16, cuda, seed=4, poison=False)
+    good = bt.clone()
+    bt[0, 1] = -5
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda)
+    keep = [0, 2]
+    kk = torch.cat([kp[int(good[0, i])] for i in keep], dim=1)[None]
+    vv = torch.cat([vp[int(good[0, i])] for i in keep], dim=1)[None]
+    ref, ref_lse = decode_attention(q, kk, vv)
+    assert_close(out, ref, ATOL[torch.bfloat16], "skip invalid")
+    assert_lse_close(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_split_count_invariance(cuda, dtype):
+    lens = [1000, 4097, 257]
+    q, kp, vp, bt, sl = _paged_case(lens, 32, 8, 128, 64, dtype, cuda, seed=5)
+    outs = [_run_paged(q, kp, vp, bt, sl, cuda, split_tokens=s) for s in (64, 256, 1024, 4160)]
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    for out, lse in outs:
+        assert_close(out, ref, ATOL[dtype], "split invariance")
+        assert_lse_close(lse, ref_lse)
+
+
+def test_decode_equals_last_prefill_row(cuda):
+    """Cross-kernel invariant: decode of token t == row t of causal prefill."""
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+    from llm_cuda.kernels.triton.decode_attention import triton_decode_attention
+
+    torch.manual_seed(11)
+    q = torch.randn(2, 8, 96, 64, device=cuda)
+    k = torch.randn(2, 2, 96, 64, device=cuda)
+    v = torch.randn(2, 2, 96, 64, device=cuda)
+    full, lfull = triton_fused_causal_attention(q, k, v, return_lse=True)
+    dec, ldec = triton_decode_attention(q[:, :, -1:].contiguous(), k, v, return_lse=True)
+    assert_close(dec[:, :, 0], full[:, :, -1], 1e-5, "decode vs prefill")
+    assert_lse_close(ldec, lfull[:, :, -1])
+
+
+def test_baseline_8b_shape_subset(cuda):
+    """BASELINE config 2 construction (seed 0, ctx ~ U[512, 8192], P 64, random
+    permutation) on 8 sequences, checked against the oracle."""
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 8193, (8,), generator=g).tolist()
+    q, kp, vp, bt, sl = _paged_case(lens, 32, 8, 128, 64, torch.bfloat16, cuda, seed=0, poison=True)
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert_close(out, ref, ATOL[torch.bfloat16], "8B subset")
+    assert_lse_close(lse, ref_lse)
+
+
+def test_baseline_70b_long_context_subset(cuda):
+    """BASELINE config 5 head layout (64/8 heads, D 128) at context 32768 on 2 sequences."""
+    lens = [32768, 32768 - 37]
+    q, kp, vp, bt, sl = _paged_case(lens, 64, 8, 128, 64, torch.bfloat16, cuda, seed=1, poison=False)
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert_close(out, ref, ATOL[torch.bfloat16], "70B subset")
+    assert_lse_close(lse, ref_lse)

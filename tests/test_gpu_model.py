@@ -1,0 +1,154 @@
+"""GPU model-level parity (the harness of BASELINE configs 1 and 4).
+
+* Config 1 (tiny Llama-3, fp32, dim 256, 4 layers, 8/2 heads, FFN 688,
+  vocab 32000, batch 2, prompt 64, 16 greedy steps, paged KV with P 64) runs
+  on the HIP kernels and is compared with the oracle's full-recompute greedy
+  decode on the same weights: identical ids, logits within 1e-4.
+* The reference's own model tests (test_llama3_shapes.py:8-198): shapes,
+  tuple-cache decode == full forward, paged decode == full forward.
+* A reduced-depth bf16 model at the 8B layer shape: paged decode logits ==
+  full-forward logits.
+"""
+import pytest
+import torch
+
+import oracle.model as omodel
+
+pytestmark = pytest.mark.gpu
+
+
+def _small_config(**kw):
+    from llm_cuda.models.llama3.config import Llama3Config
+
+    base = dict(vocab_size=1024, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                num_attention_heads=8, num_key_value_heads=4, max_position_embeddings=256)
+    base.update(kw)
+    return Llama3Config(**base)
+
+
+def test_forward_shapes_and_loss(cuda):
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(0)
+    cfg = _small_config()
+    model = Llama3ForCausalLM(cfg).to(cuda)
+    ids = torch.randint(0, cfg.vocab_size, (2, 16), device=cuda)
+    out = model(input_ids=ids, labels=ids)
+    assert out["logits"].shape == (2, 16, cfg.vocab_size)
+    assert out["loss"].dim() == 0 and torch.isfinite(out["loss"])
+
+
+def test_full_forward_matches_oracle(cuda):
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(123)
+    cfg = _small_config()
+    model = Llama3ForCausalLM(cfg).eval()
+    ids = torch.randint(0, cfg.vocab_size, (2, 12))
+    ref = omodel.forward(model.state_dict(), cfg, ids)
+    model = model.to(cuda)
+    with torch.no_grad():
+        out = model(input_ids=ids.to(cuda))["logits"]
+    assert (out.cpu() - ref).abs().max().item() < 1e-4
+
+
+def test_tuple_cache_decode_parity(cuda):
+    """test_llama3_shapes.py:47-88 on the GPU."""
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(123)
+    cfg = _small_config()
+    model = Llama3ForCausalLM(cfg).to(cuda).eval()
+    ids = torch.randint(0, cfg.vocab_size, (1, 12), device=cuda)
+    with torch.no_grad():
+        full = model(input_ids=ids)["logits"]
+        past = model(input_ids=ids[:, :8], use_cache=True)["past_key_values"]
+        steps = []
+        for i in range(8, 12):
+            o = model(input_ids=ids[:, i:i + 1], past_key_values=past, use_cache=True)
+            past = o["past_key_values"]
+            steps.append(o["logits"])
+    assert torch.allclose(torch.cat(steps, 1), full[:, 8:], atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_paged_decode_parity(cuda, batch):
+    """test_llama3_shapes.py:152-198 (page_size 4), plus batch > 1."""
+    from llm_cuda.models.llama3.kv_cache import PagedKVCache
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(126)
+    cfg = _small_config()
+    model = Llama3ForCausalLM(cfg).to(cuda).eval()
+    ids = torch.randint(0, cfg.vocab_size, (batch, 12), device=cuda)
+    cache = PagedKVCache.create(num_layers=cfg.num_hidden_layers, num_kv_heads=cfg.num_key_value_heads,
+                                head_dim=cfg.head_dim, max_seq_len=32, page_size=4, device=cuda,
+                                dtype=torch.float32, batch_size=batch)
+    with torch.no_grad():
+        full = model(input_ids=ids)["logits"]
+        model(input_ids=ids[:, :8], past_key_values=cache, use_cache=True)
+        steps = [model(input_ids=ids[:, i:i + 1], past_key_values=cache, use_cache=True)["logits"]
+                 for i in range(8, 12)]
+    assert torch.allclose(torch.cat(steps, 1), full[:, 8:], atol=1e-5, rtol=1e-5)
+
+
+def test_chunked_prefill_through_paged_cache(cuda):
+    """A prompt fed in two chunks (second chunk attends to the cached first)."""
+    from llm_cuda.models.llama3.kv_cache import PagedKVCache
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(127)
+    cfg = _small_config()
+    model = Llama3ForCausalLM(cfg).to(cuda).eval()
+    ids = torch.randint(0, cfg.vocab_size, (2, 20), device=cuda)
+    cache = PagedKVCache.create(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, 32, 8,
+                                cuda, torch.float32, batch_size=2)
+    with torch.no_grad():
+        full = model(input_ids=ids)["logits"]
+        model(input_ids=ids[:, :11], past_key_values=cache, use_cache=True)
+        tail = model(input_ids=ids[:, 11:], past_key_values=cache, use_cache=True)["logits"]
+    assert torch.allclose(tail, full[:, 11:], atol=1e-5, rtol=1e-5)
+
+
+def test_config1_tiny_llama_greedy_matches_oracle(cuda):
+    """seed 0, fp32, batch 2, prompt 64, 16 greedy steps, paged P 64."""
+    from llm_cuda.models.llama3.config import Llama3Config
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    cfg = Llama3Config(vocab_size=32000, hidden_size=256, intermediate_size=688, num_hidden_layers=4,
+                       num_attention_heads=8, num_key_value_heads=2)
+    torch.manual_seed(0)
+    model = Llama3ForCausalLM(cfg).eval()
+    prompt = torch.randint(0, cfg.vocab_size, (2, 64))
+    ref_ids, ref_logits = omodel.greedy(model.state_dict(), cfg, prompt, 16)
+    model = model.to(cuda)
+    ids = model.generate(prompt.to(cuda), max_new_tokens=16, use_paged_kv=True, page_size=64)
+    assert torch.equal(ids.cpu(), ref_ids)
+    # per-step logits of the paged run, re-derived by a full forward on the GPU
+    with torch.no_grad():
+        logits = model(input_ids=ids[:, :-1])["logits"][:, 63:, :]
+    assert (logits.transpose(0, 1).cpu() - ref_logits).abs().max().item() < 1e-4
+
+
+def test_bf16_8b_layer_shape_paged_vs_full(cuda):
+    """Two layers at the Llama-3-8B layer shape in bf16: paged decode logits match
+    the full forward (bf16 tolerance, relative to the logit scale)."""
+    from llm_cuda.models.llama3.config import Llama3Config
+    from llm_cuda.models.llama3.kv_cache import PagedKVCache
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    cfg = Llama3Config(vocab_size=2048, hidden_size=4096, intermediate_size=14336, num_hidden_layers=2,
+                       num_attention_heads=32, num_key_value_heads=8)
+    torch.manual_seed(1)
+    model = Llama3ForCausalLM(cfg).to(device=cuda, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, cfg.vocab_size, (4, 70), device=cuda)
+    cache = PagedKVCache.create(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, 128, 64,
+                                cuda, torch.bfloat16, batch_size=4)
+    with torch.no_grad():
+        full = model(input_ids=ids)["logits"].float()
+        model(input_ids=ids[:, :66], past_key_values=cache, use_cache=True)
+        steps = [model(input_ids=ids[:, i:i + 1], past_key_values=cache, use_cache=True)["logits"]
+                 for i in range(66, 70)]
+    got = torch.cat(steps, 1).float()
+    scale = full[:, 66:].abs().max().item()
+    assert (got - full[:, 66:]).abs().max().item() <= 3e-2 * max(1.0, scale)

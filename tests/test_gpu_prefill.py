@@ -1,0 +1,107 @@
+"""GPU parity: causal prefill attention (O and lse) vs the fp32 oracle.
+
+Cases follow the reference's attention tests (test_triton_attention.py,
+seeds 0/11) and add native GQA, q_offset (a cached prefix), lengths that are
+not tile multiples, every head_dim the entry accepts, and the BASELINE config-3
+shape (S 4096, 32/8 heads, D 128, RoPE theta 500000) on a head subset.
+"""
+import pytest
+import torch
+
+from helpers import ATOL, assert_close, assert_lse_close
+from oracle.attention import causal_attention
+from oracle.elementwise import apply_rope, build_rope_cache
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(B, Hq, Hkv, Sq, Skv, D, dtype, device, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, Sq, D, generator=g).to(dtype).to(device)
+    k = torch.randn(B, Hkv, Skv, D, generator=g).to(dtype).to(device)
+    v = torch.randn(B, Hkv, Skv, D, generator=g).to(dtype).to(device)
+    return q, k, v
+
+
+CASES = [
+    # B, Hq, Hkv, S, D, dtype
+    (2, 4, 4, 8, 16, torch.float32),      # reference CPU-parity shape
+    (1, 2, 2, 16, 32, torch.float16),     # reference GPU shape
+    (1, 8, 2, 100, 64, torch.bfloat16),
+    (2, 8, 2, 257, 128, torch.bfloat16),
+    (1, 4, 1, 130, 128, torch.float16),
+    (2, 32, 8, 300, 128, torch.bfloat16),
+    (1, 4, 2, 70, 48, torch.bfloat16),    # generic path (D not in {64, 128})
+    (1, 2, 1, 33, 256, torch.float32),
+    (1, 8, 8, 1, 128, torch.bfloat16),    # single token
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,dtype", CASES)
+def test_prefill_matches_oracle(cuda, B, Hq, Hkv, S, D, dtype):
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+
+    q, k, v = _qkv(B, Hq, Hkv, S, S, D, dtype, cuda, seed=S + D)
+    out, lse = triton_fused_causal_attention(q, k, v, return_lse=True)
+    assert out.shape == q.shape and out.dtype == dtype and lse.dtype == torch.float32
+    ref, ref_lse = causal_attention(q.cpu(), k.cpu(), v.cpu())
+    assert_close(out, ref, ATOL[dtype], "prefill out")
+    assert_lse_close(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("Sq,Skv", [(1, 77), (5, 128), (64, 200), (130, 131)])
+def test_prefill_with_cached_prefix(cuda, dtype, Sq, Skv):
+    """q_offset = Skv - Sq: the chunked-prefill masking of models/llama3/attention.py:63-89."""
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+
+    q, k, v = _qkv(2, 8, 2, Sq, Skv, 64, dtype, cuda, seed=Sq)
+    out, lse = triton_fused_causal_attention(q, k, v, return_lse=True, q_offset=Skv - Sq)
+    ref, ref_lse = causal_attention(q.cpu(), k.cpu(), v.cpu(), q_offset=Skv - Sq)
+    assert_close(out, ref, ATOL[dtype], "prefill offset")
+    assert_lse_close(lse, ref_lse)
+
+
+def test_prefill_strided_projection_views(cuda):
+    """q/k/v as the transposed [B, S, H, D] projection views the model produces."""
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+
+    g = torch.Generator().manual_seed(12)
+    B, S, Hq, Hkv, D = 2, 96, 8, 2, 128
+    q = torch.randn(B, S, Hq * D, generator=g).bfloat16().to(cuda).view(B, S, Hq, D).transpose(1, 2)
+    k = torch.randn(B, S, Hkv * D, generator=g).bfloat16().to(cuda).view(B, S, Hkv, D).transpose(1, 2)
+    v = torch.randn(B, S, Hkv * D, generator=g).bfloat16().to(cuda).view(B, S, Hkv, D).transpose(1, 2)
+    out = triton_fused_causal_attention(q, k, v)
+    ref, _ = causal_attention(q.cpu(), k.cpu(), v.cpu())
+    assert_close(out, ref, ATOL[torch.bfloat16], "prefill strided")
+
+
+def test_reference_extension_entry(cuda):
+    """cuda_causal_attention_extension keeps the reference's equal-shape contract."""
+    from llm_cuda.kernels.cuda.attention import cuda_causal_attention_extension
+
+    q, k, v = _qkv(1, 2, 2, 16, 32, torch.float16, cuda, seed=11)
+    out = cuda_causal_attention_extension(q, k, v)
+    ref, _ = causal_attention(q.cpu(), k.cpu(), v.cpu())
+    assert_close(out, ref, ATOL[torch.float16], "ext entry")
+    assert cuda_causal_attention_extension(q, k[:, :1], v[:, :1]) is None
+
+
+def test_baseline_prefill_shape_head_subset(cuda):
+    """S 4096, D 128, RoPE theta 500000 by the HIP RoPE kernel,
+    GQA 4:1; batch 1 and 2 kv-head groups (8 q heads) keep the oracle in seconds."""
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+    from llm_cuda.models.llama3.rotary import apply_rotary
+
+    S, D = 4096, 128
+    q, k, v = _qkv(1, 8, 2, S, S, D, torch.bfloat16, cuda, seed=0)
+    cos, sin = build_rope_cache(S, D, 500000.0, torch.bfloat16)
+    qr, kr = apply_rotary(q, k, cos.to(cuda), sin.to(cuda))
+    out, lse = triton_fused_causal_attention(qr, kr, v, return_lse=True)
+    qo = apply_rope(q.cpu(), cos, sin).bfloat16()
+    ko = apply_rope(k.cpu(), cos, sin).bfloat16()
+    # RoPE outputs must agree to the bf16 ulp before attention compares them.
+    assert_close(qr, qo, ATOL[torch.bfloat16], "rope q", rtol=2 ** -7)
+    ref, ref_lse = causal_attention(qr.cpu(), kr.cpu(), v.cpu())
+    assert_close(out, ref, ATOL[torch.bfloat16], "prefill 4096")
+    assert_lse_close(lse, ref_lse)

@@ -1,0 +1,144 @@
+"""Pins oracle.attention.causal_attention (prefill oracle) without retyping it.
+
+Checks: an fp64 triple loop on tiny shapes (written as explicit per-element
+sums, not matrix products), closed forms (row 0 returns v0; equal keys give
+the prefix mean of V; S = 1), the lse invariant o = sum_j exp(s_j - lse) v_j,
+GQA = per-head attention against kv head h // G, and q_offset equivalence
+(the last rows of a longer prompt). The reference's own CPU parity test
+(tests/test_triton_attention.py:37-47, seed 0, [2,4,8,16], atol 1e-5) is
+reproduced against the brute force.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle.attention import causal_attention
+
+
+def brute(q, k, v, q_offset=0):
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    out = torch.zeros(B, Hq, Sq, D, dtype=torch.float64)
+    lse = torch.full((B, Hq, Sq), float("-inf"), dtype=torch.float64)
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // G
+            for i in range(Sq):
+                scores = []
+                for j in range(Skv):
+                    if j > i + q_offset:
+                        break
+                    s = 0.0
+                    for d in range(D):
+                        s += float(q[b, h, i, d]) * float(k[b, kh, j, d])
+                    scores.append(s / math.sqrt(D))
+                if not scores:
+                    continue
+                m = max(scores)
+                z = sum(math.exp(s - m) for s in scores)
+                lse[b, h, i] = m + math.log(z)
+                for j, s in enumerate(scores):
+                    w = math.exp(s - m) / z
+                    for d in range(D):
+                        out[b, h, i, d] += w * float(v[b, kh, j, d])
+    return out, lse
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [(1, 2, 2, 5, 4), (2, 4, 2, 6, 3), (1, 8, 2, 4, 8)])
+def test_matches_bruteforce(B, Hq, Hkv, S, D):
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(B, Hq, S, D, generator=g)
+    k = torch.randn(B, Hkv, S, D, generator=g)
+    v = torch.randn(B, Hkv, S, D, generator=g)
+    o, lse = causal_attention(q, k, v)
+    ob, lb = brute(q, k, v)
+    assert torch.allclose(o.double(), ob, atol=1e-5)
+    assert torch.allclose(lse.double(), lb, atol=1e-5)
+
+
+def test_reference_cpu_parity_case():
+    """tests/test_triton_attention.py:37-47 (seed 0, [2,4,8,16]) against brute force."""
+    torch.manual_seed(0)
+    q = torch.randn(2, 4, 8, 16)
+    k = torch.randn(2, 4, 8, 16)
+    v = torch.randn(2, 4, 8, 16)
+    o, _ = causal_attention(q, k, v)
+    ob, _ = brute(q, k, v)
+    assert torch.allclose(o.double(), ob, atol=1e-5)
+
+
+def test_row0_is_v0_and_single_token():
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(2, 4, 7, 8, generator=g)
+    k = torch.randn(2, 2, 7, 8, generator=g)
+    v = torch.randn(2, 2, 7, 8, generator=g)
+    o, lse = causal_attention(q, k, v)
+    assert torch.allclose(o[:, 0::2, 0], v[:, :, 0], atol=1e-6)  # heads 0,2 -> kv 0,1
+    assert torch.allclose(o[:, 1::2, 0], v[:, :, 0], atol=1e-6)
+    # lse of row 0 is its only score
+    s00 = (q[:, :, 0] * k.repeat_interleave(2, dim=1)[:, :, 0]).sum(-1) / math.sqrt(8)
+    assert torch.allclose(lse[:, :, 0], s00, atol=1e-5)
+    o1, _ = causal_attention(q[:, :, :1], k[:, :, :1], v[:, :, :1])
+    assert torch.allclose(o1[:, :, 0], o[:, :, 0])
+
+
+def test_equal_keys_give_prefix_mean():
+    g = torch.Generator().manual_seed(3)
+    S, D = 9, 4
+    q = torch.randn(1, 2, S, D, generator=g)
+    k = torch.randn(1, 1, 1, D, generator=g).expand(1, 1, S, D).contiguous()
+    v = torch.randn(1, 1, S, D, generator=g)
+    o, lse = causal_attention(q, k, v)
+    prefix_mean = torch.cumsum(v[0, 0], 0) / torch.arange(1, S + 1).unsqueeze(1)
+    assert torch.allclose(o[0, 0], prefix_mean, atol=1e-5)
+    assert torch.allclose(o[0, 1], prefix_mean, atol=1e-5)
+    # lse = s + log(i + 1) for equal scores s
+    s = (q[0, :, :, :] * k[0, 0, 0]).sum(-1) / math.sqrt(D)
+    assert torch.allclose(lse[0], s + torch.log(torch.arange(1, S + 1).float()), atol=1e-5)
+
+
+def test_lse_invariant():
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 4, 12, 8, generator=g) * 3
+    k = torch.randn(1, 2, 12, 8, generator=g) * 3
+    v = torch.randn(1, 2, 12, 8, generator=g)
+    o, lse = causal_attention(q, k, v)
+    kr = k.repeat_interleave(2, 1)
+    vr = v.repeat_interleave(2, 1)
+    s = torch.einsum("bhid,bhjd->bhij", q, kr) / math.sqrt(8)
+    mask = torch.triu(torch.ones(12, 12, dtype=torch.bool), 1)
+    w = torch.exp(s - lse.unsqueeze(-1)).masked_fill(mask, 0.0)
+    assert torch.allclose(w.sum(-1), torch.ones(1, 4, 12), atol=1e-5)
+    assert torch.allclose(torch.einsum("bhij,bhjd->bhid", w, vr), o, atol=1e-5)
+
+
+def test_q_offset_equals_tail_of_full_prompt():
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 4, 10, 8, generator=g)
+    k = torch.randn(2, 2, 10, 8, generator=g)
+    v = torch.randn(2, 2, 10, 8, generator=g)
+    o_full, l_full = causal_attention(q, k, v)
+    o_tail, l_tail = causal_attention(q[:, :, 7:], k, v, q_offset=7)
+    assert torch.allclose(o_tail, o_full[:, :, 7:], atol=1e-6)
+    assert torch.allclose(l_tail, l_full[:, :, 7:], atol=1e-6)
+    ob, lb = brute(q[:, :, 7:], k, v, q_offset=7)
+    assert torch.allclose(o_tail.double(), ob, atol=1e-5)
+
+
+def test_row_chunking_is_invisible():
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(1, 2, 37, 8, generator=g)
+    k = torch.randn(1, 1, 37, 8, generator=g)
+    v = torch.randn(1, 1, 37, 8, generator=g)
+    a, la = causal_attention(q, k, v, row_chunk=5)
+    b, lb = causal_attention(q, k, v)
+    assert torch.allclose(a, b, atol=1e-6) and torch.allclose(la, lb, atol=1e-6)
+
+
+def test_empty_keys_give_zero_and_neg_inf():
+    q = torch.randn(1, 2, 3, 4)
+    k = torch.zeros(1, 1, 0, 4)
+    o, lse = causal_attention(q, k, k)
+    assert (o == 0).all() and torch.isinf(lse).all() and (lse < 0).all()
