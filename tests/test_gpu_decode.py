@@ -76,8 +76,9 @@ def _paged_case(lens, Hq, Hkv, D, P, dtype, device, seed=0, poison=True, extra_p
         for b, L in enumerate(lens):
             for t in range(L):
                 owned[bt[b, t // P], t % P] = True
-        kp[~owned] = float("nan")
-        vp[~owned] = float("nan")
+        free = (~owned)[:, None, :, None].expand_as(kp)
+        kp[free] = float("nan")
+        vp[free] = float("nan")
     q = torch.randn(len(lens), Hq, 1, D, generator=g).to(dtype)
     sl = torch.tensor(lens, dtype=torch.int32)
     return q, kp, vp, bt, sl

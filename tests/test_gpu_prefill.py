@@ -80,7 +80,7 @@ def test_reference_extension_entry(cuda):
     """cuda_causal_attention_extension keeps the reference's equal-shape contract."""
     from llm_cuda.kernels.cuda.attention import cuda_causal_attention_extension
 
-    q, k, v = _qkv(1, 2, 2, 16, 32, torch.float16, cuda, seed=11)
+    q, k, v = _qkv(1, 2, 2, 16, 16, 32, torch.float16, cuda, seed=11)
     out = cuda_causal_attention_extension(q, k, v)
     ref, _ = causal_attention(q.cpu(), k.cpu(), v.cpu())
     assert_close(out, ref, ATOL[torch.float16], "ext entry")
