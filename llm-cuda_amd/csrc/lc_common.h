@@ -90,13 +90,11 @@ __device__ __forceinline__ float lc_wave_max(float v) {
   return v;
 }
 
-// Compiler-level barrier for LDS traffic that stays inside one wavefront: the
-// hardware executes one wave's LDS instructions in order, so only compiler
-// reordering has to be prevented.
-__device__ __forceinline__ void lc_wave_lds_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+// Compiler-only barrier for LDS traffic that stays inside one wavefront. The
+// hardware executes a wave's LDS instructions in issue order, so a read issued
+// after a write sees it; only compiler reordering (e.g. of accesses through
+// differently typed pointers) must be prevented. Emits no instruction and,
+// unlike a memory-model fence, no wait on outstanding global loads.
+__device__ __forceinline__ void lc_compiler_fence() { __asm__ __volatile__("" ::: "memory"); }
 
 static inline int64_t lc_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

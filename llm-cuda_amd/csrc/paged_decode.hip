@@ -1,25 +1,28 @@
 // Split-K paged GQA flash-decode for gfx950, plus the cross-split merge.
 //
-// Work decomposition: one wavefront = one split = `split_tokens` consecutive
-// tokens of one (sequence b, kv head, group of <= 16 query heads). All G query
-// heads sharing a kv head are served by the same wave, so every K/V byte is
-// read from HBM exactly once (the reference's decode kernel re-read K/V once
-// per query head: kernels/triton/decode_attention.py:86-93,110-151).
+// Work decomposition: one wavefront (= one workgroup) = one split =
+// `split_tokens` consecutive tokens of one (sequence b, kv head, group of
+// <= 16 query heads). All G query heads sharing a kv head are served by the
+// same wave, so every K/V byte is read from HBM exactly once (the reference's
+// decode kernel re-read K/V once per query head:
+// kernels/triton/decode_attention.py:86-93,110-151).
 //
-// Per 32-token step a wave:
-//   1. computes each lane's token -> (page, slot) through the block table and
-//      issues 16-byte loads of its K and V row chunks straight from the page
-//      pool (the next step's loads are in flight while this step computes);
-//   2. S^T[16 tok x 16 heads] = K[16 tok x 32 d] * Q^T[32 d x 16 heads] on
-//      v_mfma_f32_16x16x32_{bf16,f16}, D/32 MFMAs per 16 tokens;
-//   3. online softmax in the exp2 domain (scale * log2 e folded into one
-//      multiply), max exchanged across the 4 lanes of a head by xor-shuffles;
-//   4. O^T[16 d x 16 heads] += V^T[16 d x 32 tok] * P^T[32 tok x 16 heads];
-//      V^T comes from a wave-private LDS tile (row-major write, transposed
-//      2-byte reads). P^T needs no data movement: the MFMA k index is mapped
-//      to tokens so that the S^T accumulator registers ARE the P^T operand.
-// Each split writes o/l (fp32) and its log2-domain logsumexp; the merge kernel
-// combines splits with weights 2^(lse_s - lse).
+// Main kernel (page_size a multiple of 32), per 32-token step:
+//   1. the step's K and V rows (one page, so the page id is wave-uniform) are
+//      read with fully coalesced 16-byte buffer loads (16 lanes per 256-byte
+//      row) carrying the non-temporal hint, into one register staging buffer;
+//   2. the staging buffer is copied to wave-private LDS tiles and the NEXT
+//      step's loads are issued into it at once, so they fly while this step
+//      computes from LDS;
+//   3. S^T[16 tok x 16 heads] = K[16 tok x 32 d] * Q^T[32 d x 16 heads] on
+//      v_mfma_f32_16x16x32_{bf16,f16} (K operands via ds_read_b128);
+//   4. online softmax in the exp2 domain with lazy rescaling;
+//   5. O^T[16 d x 16 heads] += V^T[16 d x 32 tok] * P^T[32 tok x 16 heads];
+//      V^T operands come from ds_read_b64_tr_b16 transposed LDS reads, and
+//      the MFMA k index is mapped to tokens so that the S^T accumulator
+//      registers ARE the P^T operand.
+// Each split writes o/l (fp32) and its log2-domain logsumexp; the merge
+// kernel combines splits with weights 2^(lse_s - lse).
 #include <math.h>
 
 #include "lc_common.h"
@@ -83,22 +86,38 @@ struct MfmaOps<f16_t> {
   }
 };
 
-constexpr int kWaves = 4;
 constexpr int kStep = 32;  // tokens per MFMA step
+// Lazy rescaling: the running reference max m_ref only moves when a new score
+// exceeds it by more than this (log2 units). Every p = 2^(s - m_ref) is then
+// <= 2^8, safe in bf16/f16 and fp32; o and l share m_ref, so o / l is exact.
+constexpr float kRescaleLog2 = 8.0f;
+// Buffer-resource word 3 for untyped (raw) buffer loads on gfx9-family parts.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of the K/V buffer loads: the non-temporal bit. Every
+// K/V byte is used exactly once, and streaming it past the caches measured
+// ~10% faster than default-policy loads for this access pattern.
+constexpr int kLoadNT = 2;
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x8_t __attribute__((ext_vector_type(8)));
+#define LC_LDS __attribute__((address_space(3)))
 
 template <typename T, int DPAD>
 struct StepRegs {
   typename MfmaOps<T>::v8 k[2][DPAD / 32];
   typename MfmaOps<T>::v8 v[2][DPAD / 32];
-  // Bit r of valid[gi]: token gi*16 + r of the step is live and has a valid
-  // page (lanes r, r+16, r+32, r+48 load the same token, so bits 0..15 suffice).
+  // Bit r of valid[gi]: token gi*16 + r of the step is live and its page is
+  // valid (lanes r, r+16, r+32, r+48 load the same token).
   uint64_t valid[2];
 };
 
+// Any page size: each lane resolves its own token's page and loads its K/V
+// chunks straight into MFMA operand layout (16 tokens x 64 contiguous bytes
+// per instruction).
 template <typename T, int DPAD>
-__device__ __forceinline__ void load_step(const DecodeArgs& a, const T* __restrict__ kp,
-                                          const T* __restrict__ vp, int b, int kvh, int t,
-                                          int t_end, int row, int q4, StepRegs<T, DPAD>& r) {
+__device__ __forceinline__ void load_step_lane(const DecodeArgs& a, const T* __restrict__ kp,
+                                               const T* __restrict__ vp, int b, int kvh, int t,
+                                               int t_end, int row, int q4, StepRegs<T, DPAD>& r) {
   typedef typename MfmaOps<T>::v8 v8;
 #pragma unroll
   for (int gi = 0; gi < 2; ++gi) {
@@ -119,136 +138,68 @@ __device__ __forceinline__ void load_step(const DecodeArgs& a, const T* __restri
   }
 }
 
-template <typename T, int DPAD>
-__global__ __launch_bounds__(64 * kWaves) void paged_decode_mfma_kernel(DecodeArgs a) {
-  typedef MfmaOps<T> Ops;
-  typedef typename Ops::v8 v8;
-  constexpr int KS = DPAD / 32;      // MFMA k-steps over head_dim
-  constexpr int DT = DPAD / 16;      // 16-row d tiles of the output
-  constexpr int LROW = DPAD + 8;     // LDS row pitch (elements), 16 B pad
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int split = blockIdx.x * kWaves + wave;
-  const int kvh = blockIdx.y / a.n_hgroups;
-  const int hg = blockIdx.y - kvh * a.n_hgroups;
-  const int b = blockIdx.z;
-  if (split >= a.max_splits) return;
-  const int len = seq_len_of(a, b);
-  const int t_begin = split * a.split_tokens;
-  if (t_begin >= len) return;
-  const int t_end = min(len, t_begin + a.split_tokens);
-
-  const int col = lane & 15;  // query head within the 16-wide tile
-  const int q4 = lane >> 4;   // 0..3
-  const int g = hg * 16 + col;
-  const bool head_ok = g < a.G;
-  const int h = kvh * a.G + g;
-
-  T* lds = reinterpret_cast<T*>(smem_raw) + wave * (kStep * LROW);
-  const T* kp = static_cast<const T*>(a.kp);
-  const T* vp = static_cast<const T*>(a.vp);
-
-  // Q^T operand: lane holds q[h, s*32 + q4*8 .. +8] for every k-step s.
-  v8 qop[KS];
-  {
-    const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+// Shared tail of both MFMA kernels: QK^T of one 32-token step is done by the
+// caller; this folds the scores into the running softmax state and returns
+// the P^T operand. sc[gi][i] are scaled, masked scores of tokens
+// gi*16 + q4*4 + i for this lane's head.
+template <typename T, int DT>
+__device__ __forceinline__ typename MfmaOps<T>::v8 softmax_step(float (&sc)[2][4], float& m_ref,
+                                                                float& l_lane, f32x4_t (&o)[DT]) {
+  typedef typename MfmaOps<T>::v8 v8;
+  float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                   fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (__ballot(mx > m_ref + kRescaleLog2)) {  // wave-uniform, rare after the first step
+    const float m_new = fmaxf(m_ref, mx);
+    const float alpha = m_new == -INFINITY ? 1.f : lc_exp2(m_ref - m_new);
+    l_lane *= alpha;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int d0 = s * 32 + q4 * 8;
-      qop[s] = (head_ok && d0 < a.D) ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
-    }
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
+    m_ref = m_new;
   }
-
-  f32x4_t o[DT];
+  const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+  v8 pop;
 #pragma unroll
-  for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;
-  float l_lane = 0.f;
-
-  auto compute_step = [&](const StepRegs<T, DPAD>& r) {
-    // Scores S^T: rows = tokens (q4*4 + i within each 16-token group), cols = heads.
-    f32x4_t sacc[2];
+  for (int gi = 0; gi < 2; ++gi)
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      sacc[gi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) sacc[gi] = Ops::mma(r.k[gi][s], qop[s], sacc[gi]);
+    for (int i = 0; i < 4; ++i) {
+      const float p = lc_exp2(sc[gi][i] - m_use);
+      l_lane += p;
+      pop[gi * 4 + i] = static_cast<T>(p);
     }
-    // V tile -> LDS (row-major [32 tok][LROW]) while the MFMAs drain.
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        *reinterpret_cast<v8*>(lds + (gi * 16 + col) * LROW + s * 32 + q4 * 8) = r.v[gi][s];
+  return pop;
+}
 
-    float sc[2][4];
-    float mx = -INFINITY;
+// O^T += V^T * P^T for one 32-token step from a row-major LDS V tile.
+// ds_read_b64_tr_b16 semantics (per 16-lane group): lane i receives element
+// i % 4 of the 8-byte chunks addressed by lanes 4e + i / 4, e = 0..3. So lane
+// 4e + c points at V[token(q4, e)][dt*16 + 4c] and lane i gets the column
+// {V[token(q4, e)][dt*16 + i] : e = 0..3}.
+template <typename T, int DT, int LROW>
+__device__ __forceinline__ void pv_step(const T* lds_v, int q4, int col,
+                                        typename MfmaOps<T>::v8 pop, f32x4_t (&o)[DT]) {
+  typedef typename MfmaOps<T>::v8 v8;
+  const int tr_e = col >> 2, tr_c = col & 3;
+  LC_LDS const short* base = (LC_LDS const short*)(lds_v);
+  const int r1 = (q4 * 4 + tr_e) * LROW + 4 * tr_c;       // tokens 4*q4 .. 4*q4+3
+  const int r2 = (16 + q4 * 4 + tr_e) * LROW + 4 * tr_c;  // tokens 16+4*q4 .. +3
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool live = (r.valid[gi] >> (q4 * 4 + i)) & 1;
-        const float v = sacc[gi][i] * a.scale_log2;
-        sc[gi][i] = live ? v : -INFINITY;
-        mx = fmaxf(mx, sc[gi][i]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = lc_exp2(m_run - m_use);
-    m_run = m_new;
-
-    float psum = 0.f;
-    v8 pop;
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = lc_exp2(sc[gi][i] - m_use);
-        psum += p;
-        pop[gi * 4 + i] = static_cast<T>(p);
-      }
-    l_lane = l_lane * alpha + psum;
-
-    lc_wave_lds_fence();
-    // V^T operand for d tile dt: lane holds V[tok(q4, j)][dt*16 + col], with
-    // tok(q4, j) = q4*4 + j (j < 4) or 16 + q4*4 + (j - 4) (j >= 4).
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      v8 vop;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tr = (j < 4) ? (q4 * 4 + j) : (16 + q4 * 4 + (j - 4));
-        vop[j] = lds[tr * LROW + dt * 16 + col];
-      }
-      f32x4_t acc = o[dt];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= alpha;
-      o[dt] = Ops::mma(vop, pop, acc);
-    }
-    lc_wave_lds_fence();
-  };
-
-  StepRegs<T, DPAD> ra, rb;
-  load_step<T, DPAD>(a, kp, vp, b, kvh, t_begin, t_end, col, q4, ra);
-  int t = t_begin;
-  while (true) {
-    const bool more_a = t + kStep < t_end;
-    if (more_a) load_step<T, DPAD>(a, kp, vp, b, kvh, t + kStep, t_end, col, q4, rb);
-    compute_step(ra);
-    if (!more_a) break;
-    t += kStep;
-    const bool more_b = t + kStep < t_end;
-    if (more_b) load_step<T, DPAD>(a, kp, vp, b, kvh, t + kStep, t_end, col, q4, ra);
-    compute_step(rb);
-    if (!more_b) break;
-    t += kStep;
+  for (int dt = 0; dt < DT; ++dt) {
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(base + r1 + dt * 16));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(base + r2 + dt * 16));
+    const i16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    o[dt] = MfmaOps<T>::mma(__builtin_bit_cast(v8, both), pop, o[dt]);
   }
+}
 
-  // Finalise this split: l summed over the 4 lanes of each head.
+// Writes this split's normalised partial output and log2-domain lse.
+template <int DT>
+__device__ __forceinline__ void store_partial(const DecodeArgs& a, int b, int h, int split,
+                                              bool head_ok, int q4, float m_ref, float l_lane,
+                                              const f32x4_t (&o)[DT]) {
   float l_tot = l_lane + __shfl_xor(l_lane, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (!head_ok) return;
@@ -258,18 +209,210 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_mfma_kernel(DecodeAr
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
     const int d0 = dt * 16 + q4 * 4;
-    if (d0 < a.D) {
+    if (d0 < a.D) {  // D % 8 == 0 on the MFMA path: 4-float groups are whole
       f32x4_t w = o[dt];
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] *= inv_l;
-      if (d0 + 4 <= a.D) {
-        *reinterpret_cast<f32x4_t*>(po + d0) = w;
-      } else {
-        for (int i = 0; i < 4 && d0 + i < a.D; ++i) po[d0 + i] = w[i];
-      }
+      *reinterpret_cast<f32x4_t*>(po + d0) = w;
     }
   }
-  if (q4 == 0) a.part_lse[pidx] = l_tot > 0.f ? m_run + lc_log2(l_tot) : -INFINITY;
+  if (q4 == 0) a.part_lse[pidx] = l_tot > 0.f ? m_ref + lc_log2(l_tot) : -INFINITY;
+}
+
+// Main kernel: page_size % 32 == 0 (every step inside one page).
+template <typename T, int DPAD>
+__global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
+  typedef MfmaOps<T> Ops;
+  typedef typename Ops::v8 v8;
+  constexpr int KS = DPAD / 32;      // MFMA k-steps over head_dim
+  constexpr int DT = DPAD / 16;      // 16-row d tiles of the output
+  constexpr int CPR = DPAD / 8;      // 16-byte chunks per token row
+  constexpr int RPI = 64 / CPR;      // token rows per load instruction
+  constexpr int NI = kStep / RPI;    // load instructions per tensor per step
+  constexpr int LROW = DPAD + 16;    // LDS row pitch (elements): rows 8 banks apart
+  __shared__ __align__(16) T lds_k[kStep * LROW];
+  __shared__ __align__(16) T lds_v[kStep * LROW];
+
+  const int lane = threadIdx.x;
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y / a.n_hgroups;
+  const int hg = blockIdx.y - kvh * a.n_hgroups;
+  const int b = blockIdx.z;
+  const int len = seq_len_of(a, b);
+  const int t_begin = split * a.split_tokens;
+  if (t_begin >= len) return;
+  const int t_end = min(len, t_begin + a.split_tokens);
+
+  const int col = lane & 15;  // query head within the 16-wide tile / token row of operands
+  const int q4 = lane >> 4;   // 0..3
+  const int g = hg * 16 + col;
+  const bool head_ok = g < a.G;
+  const int h = kvh * a.G + g;
+  const int srow = lane / CPR;    // staging: token row within a load instruction
+  const int schunk = lane % CPR;  // staging: 16-byte chunk within the row
+  const bool chunk_in_d = schunk * 8 < a.D;
+
+  // Block-table entries of this split, one per lane.
+  const int first_page = a.p_shift >= 0 ? (t_begin >> a.p_shift) : (t_begin / a.P);
+  const int last_page = a.p_shift >= 0 ? ((t_end - 1) >> a.p_shift) : ((t_end - 1) / a.P);
+  const int my_page =
+      first_page + lane <= last_page ? a.bt[(int64_t)b * a.bt_stride + first_page + lane] : -1;
+
+  v8 qop[KS];
+  {
+    const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d0 = s * 32 + q4 * 8;
+      qop[s] = (head_ok && d0 < a.D) ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
+    }
+  }
+  f32x4_t o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -INFINITY;
+  float l_lane = 0.f;
+
+  u32x4_t sk[NI], sv[NI];
+  // Issue the loads of the step starting at t. Past the split end (the
+  // prefetch after the last step) every offset is out of range: zeros, no
+  // memory traffic, and no branch for the wait-count bookkeeping to merge.
+  auto issue = [&](int t) -> bool {
+    const int page_idx = a.p_shift >= 0 ? (t >> a.p_shift) : (t / a.P);
+    const int slot0 = t - page_idx * a.P;
+    const bool in_split = t < t_end;
+    const int phys = __builtin_amdgcn_readlane(my_page, in_split ? page_idx - first_page : 0);
+    const bool pvalid =
+        in_split && static_cast<unsigned>(phys) < static_cast<unsigned>(a.num_pages);
+    const int64_t base = pvalid ? (int64_t)phys * a.s_page + (int64_t)kvh * a.s_head : 0;
+    const int nbytes =
+        pvalid ? static_cast<int>(((int64_t)(a.P - 1) * a.s_tok + a.D) * sizeof(T)) : 0;
+    const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(static_cast<const T*>(a.kp) + base), 0, nbytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(static_cast<const T*>(a.vp) + base), 0, nbytes, kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = i * RPI + srow;
+      const bool live = pvalid && t + row < t_end && chunk_in_d;
+      const int off =
+          live ? static_cast<int>(((int64_t)(slot0 + row) * a.s_tok + schunk * 8) * sizeof(T))
+               : -16;
+      sk[i] = __builtin_amdgcn_raw_buffer_load_b128(rK, off, 0, kLoadNT);
+      sv[i] = __builtin_amdgcn_raw_buffer_load_b128(rV, off, 0, kLoadNT);
+    }
+    return pvalid;
+  };
+
+  bool pvalid = issue(t_begin);
+  for (int t = t_begin; t < t_end; t += kStep) {
+    // staging -> LDS (row-major [32 tok][LROW])
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = i * RPI + srow;
+      *reinterpret_cast<u32x4_t*>(lds_k + row * LROW + schunk * 8) = sk[i];
+      *reinterpret_cast<u32x4_t*>(lds_v + row * LROW + schunk * 8) = sv[i];
+    }
+    const bool cur_valid = pvalid;
+    pvalid = issue(t + kStep);
+    lc_compiler_fence();
+
+    f32x4_t sacc[2];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      sacc[gi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const v8 kop = *reinterpret_cast<const v8*>(lds_k + (gi * 16 + col) * LROW + s * 32 + q4 * 8);
+        sacc[gi] = Ops::mma(kop, qop[s], sacc[gi]);
+      }
+    }
+    float sc[2][4];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool live = cur_valid && t + gi * 16 + q4 * 4 + i < t_end;
+        sc[gi][i] = live ? sacc[gi][i] * a.scale_log2 : -INFINITY;
+      }
+    const v8 pop = softmax_step<T, DT>(sc, m_ref, l_lane, o);
+    pv_step<T, DT, LROW>(lds_v, q4, col, pop, o);
+    lc_compiler_fence();
+  }
+  store_partial<DT>(a, b, h, split, head_ok, q4, m_ref, l_lane, o);
+}
+
+// Page sizes that are not multiples of 32: per-lane page resolution.
+template <typename T, int DPAD>
+__global__ __launch_bounds__(64) void paged_decode_lanes_kernel(DecodeArgs a) {
+  typedef MfmaOps<T> Ops;
+  typedef typename Ops::v8 v8;
+  constexpr int KS = DPAD / 32;
+  constexpr int DT = DPAD / 16;
+  constexpr int LROW = DPAD + 16;
+  __shared__ __align__(16) T lds_v[kStep * LROW];
+
+  const int lane = threadIdx.x;
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y / a.n_hgroups;
+  const int hg = blockIdx.y - kvh * a.n_hgroups;
+  const int b = blockIdx.z;
+  const int len = seq_len_of(a, b);
+  const int t_begin = split * a.split_tokens;
+  if (t_begin >= len) return;
+  const int t_end = min(len, t_begin + a.split_tokens);
+  const int col = lane & 15;
+  const int q4 = lane >> 4;
+  const int g = hg * 16 + col;
+  const bool head_ok = g < a.G;
+  const int h = kvh * a.G + g;
+  const T* kp = static_cast<const T*>(a.kp);
+  const T* vp = static_cast<const T*>(a.vp);
+
+  v8 qop[KS];
+  {
+    const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d0 = s * 32 + q4 * 8;
+      qop[s] = (head_ok && d0 < a.D) ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
+    }
+  }
+  f32x4_t o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -INFINITY;
+  float l_lane = 0.f;
+
+  for (int t = t_begin; t < t_end; t += kStep) {
+    StepRegs<T, DPAD> r;
+    load_step_lane<T, DPAD>(a, kp, vp, b, kvh, t, t_end, col, q4, r);
+    f32x4_t sacc[2];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      sacc[gi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) sacc[gi] = Ops::mma(r.k[gi][s], qop[s], sacc[gi]);
+    }
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        *reinterpret_cast<v8*>(lds_v + (gi * 16 + col) * LROW + s * 32 + q4 * 8) = r.v[gi][s];
+    float sc[2][4];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool live = (r.valid[gi] >> (q4 * 4 + i)) & 1;
+        sc[gi][i] = live ? sacc[gi][i] * a.scale_log2 : -INFINITY;
+      }
+    const v8 pop = softmax_step<T, DT>(sc, m_ref, l_lane, o);
+    lc_compiler_fence();
+    pv_step<T, DT, LROW>(lds_v, q4, col, pop, o);
+    lc_compiler_fence();
+  }
+  store_partial<DT>(a, b, h, split, head_ok, q4, m_ref, l_lane, o);
 }
 
 // Generic decode: one wave per (b, query head, split), lanes across head_dim,
@@ -330,12 +473,16 @@ __global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) 
   if (lane == 0) a.part_lse[pidx] = l_run > 0.f ? m_run + lc_log2(l_run) : -INFINITY;
 }
 
-// Cross-split merge: one wave per (b, h). lse = log2-sum-exp2 of split lses,
-// out = sum_s 2^(lse_s - lse) * o_s. Writes the natural-log lse.
-template <typename T>
+// Cross-split merge: one wave per (b, h). Lanes take one split each to form
+// the weights 2^(lse_s - max) in parallel; the weighted sum then walks the
+// splits 8 at a time with independent, unpredicated row loads (each lane owns
+// VPL consecutive floats of head_dim), so its latency is a few round trips.
+// out = sum_s w_s o_s / sum_s w_s; lse = (max + log2 sum_s w_s) * ln 2.
+template <typename T, int VPL>
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, T* __restrict__ out,
                                                           int64_t o_sb, int64_t o_sh,
                                                           float* __restrict__ lse_out) {
+  constexpr int kBatch = 8;
   const int lane = threadIdx.x;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
@@ -343,66 +490,87 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, T* __res
   const int nsplit = (len + a.split_tokens - 1) / a.split_tokens;
   const int64_t pbase = ((int64_t)b * a.Hq + h) * a.max_splits;
   T* oh = out + (int64_t)b * o_sb + (int64_t)h * o_sh;
+  const int d0 = lane * VPL;
+  const int dl = d0 < a.D ? d0 : 0;  // lanes past head_dim read (and drop) column 0
 
   float mx = -INFINITY;
   for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, a.part_lse[pbase + s]);
   mx = lc_wave_max(mx);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  float wsum = 0.f;
-  if (mx != -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
-      const float ls = a.part_lse[pbase + s];
-      const float w = lc_exp2(ls - mx);
-      wsum += w;
-      const float* po = a.part_o + (pbase + s) * a.D;
+  float acc[VPL];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        if (d < a.D) acc[i] = fmaf(w, po[d], acc[i]);
+  for (int e = 0; e < VPL; ++e) acc[e] = 0.f;
+  float wlane = 0.f;
+  if (mx != -INFINITY) {
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+      const int n = min(64, nsplit - s0);
+      const float w = lane < n ? lc_exp2(a.part_lse[pbase + s0 + lane] - mx) : 0.f;
+      wlane += w;
+      const float* rows = a.part_o + (pbase + s0) * a.D + dl;
+      for (int j0 = 0; j0 < n; j0 += kBatch) {
+        float v[kBatch][VPL];
+#pragma unroll
+        for (int jj = 0; jj < kBatch; ++jj) {
+          const int j = min(j0 + jj, n - 1);
+#pragma unroll
+          for (int e = 0; e < VPL; ++e) v[jj][e] = rows[(int64_t)j * a.D + e];
+        }
+#pragma unroll
+        for (int jj = 0; jj < kBatch; ++jj) {
+          const float wj = __int_as_float(
+              __builtin_amdgcn_readlane(__float_as_int(w), min(j0 + jj, 63)));
+          const float wk = j0 + jj < n ? wj : 0.f;
+#pragma unroll
+          for (int e = 0; e < VPL; ++e) acc[e] = fmaf(wk, v[jj][e], acc[e]);
+        }
       }
     }
   }
+  const float wsum = lc_wave_sum(wlane);
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int d = lane + 64 * i;
-    if (d < a.D) oh[d] = lc_from_f32<T>(acc[i] * inv);
-  }
+  for (int e = 0; e < VPL; ++e)
+    if (d0 + e < a.D) oh[d0 + e] = lc_from_f32<T>(acc[e] * inv);
   if (lse_out != nullptr && lane == 0)
     lse_out[(int64_t)b * a.Hq + h] = wsum > 0.f ? (mx + lc_log2(wsum)) * kLn2 : -INFINITY;
 }
 
 template <typename T, int DPAD>
-int launch_mfma(const DecodeArgs& a, hipStream_t st) {
-  const size_t lds = (size_t)kWaves * kStep * (DPAD + 8) * sizeof(T);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&paged_decode_mfma_kernel<T, DPAD>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess)
-      return lc_fail(static_cast<int>(e), "lc_paged_decode_fwd: LDS attribute: %s",
-                     hipGetErrorString(e));
-    attr_set = true;
-  }
-  dim3 grid((a.max_splits + kWaves - 1) / kWaves, a.Hkv * a.n_hgroups, a.B);
-  paged_decode_mfma_kernel<T, DPAD><<<grid, 64 * kWaves, lds, st>>>(a);
+int launch_mfma(const DecodeArgs& a, bool rows, hipStream_t st) {
+  dim3 grid(a.max_splits, a.Hkv * a.n_hgroups, a.B);
+  if (rows)
+    paged_decode_rows_kernel<T, DPAD><<<grid, 64, 0, st>>>(a);
+  else
+    paged_decode_lanes_kernel<T, DPAD><<<grid, 64, 0, st>>>(a);
   return lc_check_launch("lc_paged_decode_fwd (mfma)");
 }
 
 template <typename T>
+int launch_merge(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, float* lse,
+                 hipStream_t st) {
+  dim3 mgrid(a.Hq, a.B);
+  T* o = static_cast<T*>(out);
+  if (a.D <= 64)
+    decode_merge_kernel<T, 1><<<mgrid, 64, 0, st>>>(a, o, o_sb, o_sh, lse);
+  else if (a.D <= 128)
+    decode_merge_kernel<T, 2><<<mgrid, 64, 0, st>>>(a, o, o_sb, o_sh, lse);
+  else
+    decode_merge_kernel<T, 4><<<mgrid, 64, 0, st>>>(a, o, o_sb, o_sh, lse);
+  return lc_check_launch("lc_paged_decode_fwd (merge)");
+}
+
+template <typename T>
 int launch_decode(DecodeArgs a, void* out, int64_t o_sb, int64_t o_sh, float* lse, bool mfma,
-                  hipStream_t st) {
+                  bool rows, hipStream_t st) {
   int rc = LC_OK;
   if (mfma) {
     if constexpr (sizeof(T) == 2) {
       a.n_hgroups = (a.G + 15) / 16;
       if (a.D <= 64)
-        rc = launch_mfma<T, 64>(a, st);
+        rc = launch_mfma<T, 64>(a, rows, st);
       else if (a.D <= 128)
-        rc = launch_mfma<T, 128>(a, st);
+        rc = launch_mfma<T, 128>(a, rows, st);
       else
-        rc = launch_mfma<T, 256>(a, st);
+        rc = launch_mfma<T, 256>(a, rows, st);
     }
   } else {
     dim3 grid(a.max_splits, a.Hq, a.B);
@@ -410,9 +578,7 @@ int launch_decode(DecodeArgs a, void* out, int64_t o_sb, int64_t o_sh, float* ls
     rc = lc_check_launch("lc_paged_decode_fwd (generic)");
   }
   if (rc != LC_OK) return rc;
-  dim3 mgrid(a.Hq, a.B);
-  decode_merge_kernel<T><<<mgrid, 64, 0, st>>>(a, static_cast<T*>(out), o_sb, o_sh, lse);
-  return lc_check_launch("lc_paged_decode_fwd (merge)");
+  return launch_merge<T>(a, out, o_sb, o_sh, lse, st);
 }
 
 }  // namespace
@@ -496,15 +662,19 @@ int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                     kv_s_page % 8 == 0 && kv_s_head % 8 == 0 && kv_s_tok % 8 == 0 &&
                     lc_aligned(q, 16) && lc_aligned(key_pages, 16) &&
                     lc_aligned(value_pages, 16);
-  (void)esz;
+  // Row kernel: every 32-token step stays inside one page, a split touches at
+  // most 64 pages (one per lane), and a page's head slice is addressable with
+  // 31-bit byte offsets.
+  const bool rows = page_size % 32 == 0 && split_tokens / page_size + 1 <= 64 &&
+                    ((page_size - 1) * kv_s_tok + D) * esz < (1LL << 31);
   hipStream_t st = lc_stream(stream);
   switch (dtype) {
     case LC_DTYPE_F32:
-      return launch_decode<float>(a, out, o_sb, o_sh, lse, false, st);
+      return launch_decode<float>(a, out, o_sb, o_sh, lse, false, false, st);
     case LC_DTYPE_BF16:
-      return launch_decode<bf16_t>(a, out, o_sb, o_sh, lse, mfma, st);
+      return launch_decode<bf16_t>(a, out, o_sb, o_sh, lse, mfma, rows, st);
     case LC_DTYPE_F16:
-      return launch_decode<f16_t>(a, out, o_sb, o_sh, lse, mfma, st);
+      return launch_decode<f16_t>(a, out, o_sb, o_sh, lse, mfma, rows, st);
     default:
       return lc_fail(LC_EINVAL, "lc_paged_decode_fwd: unknown dtype %d", dtype);
   }

@@ -190,14 +190,12 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offse
 def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens: int) -> int:
     """Tokens per split-K wave.
 
-    A split's partial output costs 2 * G * D * 4 bytes of workspace traffic
-    against split * D * 4 bytes of K/V, so splits of ~64*G tokens keep that
-    overhead near 3%; smaller splits are used only when the grid would
-    otherwise leave the 256 CUs (2 resident waves per SIMD) idle.
+    512-token splits measured fastest at both BASELINE decode shapes (a split's
+    partial output costs 2 * G * D * 4 bytes of workspace traffic against
+    512 * D * 4 bytes of K/V, ~1.6% at G = 8); smaller splits are used only when
+    the grid would otherwise leave the 256 CUs idle.
     """
-    split = 64
-    while split < 64 * max(1, group) and split < 1024:
-        split *= 2
+    split = 512
     units = batch * n_kv_heads * ((group + 15) // 16)
     while split > 64 and units * ((capacity_tokens + split - 1) // split) < 2048:
         split //= 2

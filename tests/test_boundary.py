@@ -172,8 +172,8 @@ def test_kv_cache_argument_checks():
 def test_split_heuristic():
     from llm_cuda.kernels._ops import choose_split_tokens
 
-    # 8B decode shape: G = 4 -> 256-token splits; 70B long context: G = 8 -> 512.
-    assert choose_split_tokens(64, 8, 4, 8192) == 256
+    # both BASELINE decode shapes use 512-token splits
+    assert choose_split_tokens(64, 8, 4, 8192) == 512
     assert choose_split_tokens(8, 8, 8, 32768) == 512
     # tiny batch: splits shrink to keep the grid busy, never below 64.
     assert choose_split_tokens(1, 2, 4, 128) == 64
