@@ -1,9 +1,9 @@
 // Causal attention forward (prefill) with native GQA and logsumexp output.
 //
 // Two kernels, chosen by dtype and head_dim:
-//   * prefill_mfma_kernel (bf16/f16, D in {64, 128}): flash attention on
-//     v_mfma_f32_16x16x32_{bf16,f16} with K/V tiles double-buffered in LDS
-//     (prefill_mfma.inc).
+//   * prefill_mfma_kernel (bf16/f16, D a multiple of 8 up to 128): flash
+//     attention on v_mfma_f32_32x32x16_{bf16,f16} with K/V tiles
+//     double-buffered through LDS.
 //   * prefill_generic_kernel (everything else, incl. fp32): one lane per query
 //     row, fp32 FMA, K/V tiles staged through LDS.
 // Both compute, for query row i of (b, h) and keys j < Skv with
@@ -92,6 +92,274 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
     a.lse[((int64_t)b * a.Hq + h) * a.Sq + i] = l > 0.f ? (m + lc_log2(l)) * kLn2 : -INFINITY;
 }
 
+// ---------------------------------------------------------------------------
+// MFMA kernel (bf16/f16, D in {64, 128}).
+//
+// Workgroup = 4 waves that share one kv head: wave w computes 32 query rows of
+// one q head. The workgroup covers HW = gcd(G, 4) heads of the kv group times
+// 4 / HW blocks of 32 rows (G = 4: the group's 4 heads on the same rows), so
+// every K/V tile staged in LDS feeds 4 waves.
+//
+// Per 64-key tile and wave:
+//   S^T[32 keys x 32 q] = K[32 keys x 16 d] * Q^T[16 d x 32 q], D/16 k-steps
+//   per 32-key half, on v_mfma_f32_32x32x16_{bf16,f16}. Q^T stays in
+//   registers (lane: query row l % 32, d = (l / 32) * D/2 + 8s .. +8); K
+//   operands are ds_read_b128 of K rows in the same d order.
+//   Keys land on accumulator rows (8j + 4h + i, h = l / 32) and queries on
+//   lanes, so a query's max/sum over keys is 16 in-lane values + 1 shuffle.
+//   O^T[32 d x 32 q] += V^T[32 d x 16 keys] * P^T[16 keys x 32 q]: the MFMA k
+//   index h*8 + jj*4 + i is mapped to key 16jp + 8jj + 4h + i, so each lane's
+//   P^T operand is its own S^T registers (rounded to bf16/f16); V^T operands
+//   come from ds_read_b64_tr_b16 (4 keys x 16 d per 16-lane group).
+// K/V tiles are double-buffered: the next tile's global loads are in flight
+// (registers) while the current tile computes from LDS.
+// ---------------------------------------------------------------------------
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x8_t __attribute__((ext_vector_type(8)));
+#define LC_LDS __attribute__((address_space(3)))
+
+template <typename T>
+struct Mfma32;
+template <>
+struct Mfma32<bf16_t> {
+  typedef bf16x8_t v8;
+  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma32<f16_t> {
+  typedef f16x8_t v8;
+  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kPfWaves = 4;
+constexpr int kPfRows = 32;     // query rows per wave
+constexpr int kPfKeys = 64;     // keys per tile
+constexpr float kPfRescaleLog2 = 8.0f;
+
+template <typename T, int DPAD>
+__global__ __launch_bounds__(64 * kPfWaves) void prefill_mfma_kernel(PrefillArgs a, int hw,
+                                                                     int n_rbg) {
+  typedef Mfma32<T> Ops;
+  typedef typename Ops::v8 v8;
+  constexpr int KS = DPAD / 16;          // QK^T k-steps (16 d each)
+  constexpr int DTL = DPAD / 32;         // 32-row d tiles of O^T
+  constexpr int LROW = DPAD + 8;         // LDS row pitch (elements)
+  constexpr int TILE = kPfKeys * LROW;   // elements per K or V tile buffer
+  constexpr int CPR = DPAD / 8;          // 16-byte chunks per row
+  constexpr int LPT = kPfKeys * CPR / (64 * kPfWaves);  // 16-byte loads per thread per tensor
+  __shared__ __align__(16) T lds[2][2][TILE];  // [buffer][K, V][tile]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+  const int rbw = kPfWaves / hw;
+  // Heaviest (latest) row groups first: causal work grows with the row index.
+  const int rbg = n_rbg - 1 - (int)blockIdx.x;
+  const int n_hg = a.G / hw;
+  const int kvh = blockIdx.y / n_hg;
+  const int hgi = blockIdx.y - kvh * n_hg;
+  const int b = blockIdx.z;
+  const int head = kvh * a.G + hgi * hw + (wave % hw);
+  const int r0 = (rbg * rbw + wave / hw) * kPfRows;
+  const int wg_last_row = min(a.Sq - 1, (rbg * rbw + rbw) * kPfRows - 1);
+  const int kv_end = min(a.Skv, wg_last_row + a.q_offset + 1);  // keys any wave needs
+  const int my_kv_end = min(a.Skv, min(a.Sq - 1, r0 + kPfRows - 1) + a.q_offset + 1);
+  const bool wave_active = r0 < a.Sq;
+
+  const T* qbase = static_cast<const T*>(a.q) + b * a.qs[0] + (int64_t)head * a.qs[1];
+  const T* kbase = static_cast<const T*>(a.k) + b * a.ks[0] + (int64_t)kvh * a.ks[1];
+  const T* vbase = static_cast<const T*>(a.v) + b * a.vs[0] + (int64_t)kvh * a.vs[1];
+
+  // Q^T operand registers.
+  v8 qop[KS];
+  {
+    const int qi = r0 + l32;
+    const bool ok = wave_active && qi < a.Sq;
+    const T* qrow = qbase + (int64_t)qi * a.qs[2] + hh * (DPAD / 2);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d = hh * (DPAD / 2) + s * 8;
+      qop[s] = (ok && d < a.D) ? *reinterpret_cast<const v8*>(qrow + s * 8) : v8{};
+    }
+  }
+
+  f32x16_t o[DTL];
+#pragma unroll
+  for (int i = 0; i < DTL; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m_ref = -INFINITY, l_lane = 0.f;
+  const int qi = r0 + l32;
+
+  // Tile staging: thread tid loads chunks c = tid + 256 * u of the K and V tile.
+  u32x4_t stk[LPT], stv[LPT];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int c = tid + 64 * kPfWaves * u;
+      const int row = c / CPR, ch = c - row * CPR;
+      const int key = k0 + row;
+      const bool ok = key < kv_end && ch * 8 < a.D;
+      stk[u] = ok ? *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * a.ks[2] + ch * 8)
+                  : u32x4_t{0, 0, 0, 0};
+      stv[u] = ok ? *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * a.vs[2] + ch * 8)
+                  : u32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int c = tid + 64 * kPfWaves * u;
+      const int row = c / CPR, ch = c - row * CPR;
+      *reinterpret_cast<u32x4_t*>(&lds[buf][0][row * LROW + ch * 8]) = stk[u];
+      *reinterpret_cast<u32x4_t*>(&lds[buf][1][row * LROW + ch * 8]) = stv[u];
+    }
+  };
+
+  const int n_tiles = (kv_end + kPfKeys - 1) / kPfKeys;
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    const int k0 = it * kPfKeys;
+    const bool more = it + 1 < n_tiles;
+    if (more) load_tile(k0 + kPfKeys);
+
+    if (wave_active && k0 < my_kv_end) {
+      const T* kt_lds = &lds[buf][0][0];
+      const T* vt_lds = &lds[buf][1][0];
+      // S^T for the two 32-key halves.
+      f32x16_t sacc[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+        const T* krow = kt_lds + (kt * 32 + l32) * LROW + hh * (DPAD / 2);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          sacc[kt] = Ops::mma(*reinterpret_cast<const v8*>(krow + s * 8), qop[s], sacc[kt]);
+      }
+      // Scale and mask: key k0 + kt*32 + 8j + 4hh + i vs query qi.
+      const bool need_mask = k0 + kPfKeys > min(a.Skv, r0 + a.q_offset + 1);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = sacc[kt][r] * a.scale_log2;
+          if (need_mask) {
+            const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+            if (key > qi + a.q_offset || key >= a.Skv) v = -INFINITY;
+          }
+          sacc[kt][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (__ballot(mx > m_ref + kPfRescaleLog2)) {
+        const float m_new = fmaxf(m_ref, mx);
+        const float alpha = m_new == -INFINITY ? 1.f : lc_exp2(m_ref - m_new);
+        l_lane *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+      // P^T operands: step (kt, jp) takes accumulator rows j = 2jp, 2jp + 1.
+      v8 pop[2][2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = lc_exp2(sacc[kt][r] - m_use);
+          l_lane += p;
+          pop[kt][r >> 3][r & 7] = static_cast<T>(p);
+        }
+      // O^T += V^T P^T. Transposed reads: 16-lane group gq = lane / 16 covers
+      // keys 4hh .. 4hh+3 (+8jj, +16jp, +32kt) and d = dt*32 + (gq & 1)*16 .. +15.
+      const int gq = lane >> 4;
+      const int e = (lane & 15) >> 2, c = lane & 3;
+      LC_LDS const short* vs = (LC_LDS const short*)(vt_lds);
+      const int vrow0 = (hh * 4 + e) * LROW + (gq & 1) * 16 + 4 * c;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          const int rbase = vrow0 + (kt * 32 + jp * 16) * LROW;
+#pragma unroll
+          for (int dt = 0; dt < DTL; ++dt) {
+            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (LC_LDS i16x4_t*)(vs + rbase + dt * 32));
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (LC_LDS i16x4_t*)(vs + rbase + 8 * LROW + dt * 32));
+            const i16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            o[dt] = Ops::mma(__builtin_bit_cast(v8, both), pop[kt][jp], o[dt]);
+          }
+        }
+    }
+    if (more) {
+      store_tile(buf ^ 1);
+    }
+    __syncthreads();
+  }
+
+  if (!wave_active) return;
+  float l_tot = l_lane + __shfl_xor(l_lane, 32, 64);
+  const bool row_ok = qi < a.Sq;
+  if (!row_ok) return;
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  T* orow = static_cast<T*>(a.o) + b * a.os[0] + (int64_t)head * a.os[1] + (int64_t)qi * a.os[2];
+#pragma unroll
+  for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = dt * 32 + j * 8 + hh * 4;
+      if (d < a.D) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = lc_from_f32<T>(o[dt][j * 4 + i] * inv);
+        *reinterpret_cast<t4*>(orow + d) = w;
+      }
+    }
+  if (a.lse != nullptr && hh == 0)
+    a.lse[((int64_t)b * a.Hq + head) * a.Sq + qi] =
+        l_tot > 0.f ? (m_ref + lc_log2(l_tot)) * kLn2 : -INFINITY;
+}
+
+static int gcd_int(int x, int y) {
+  while (y) {
+    const int t = x % y;
+    x = y;
+    y = t;
+  }
+  return x;
+}
+
+template <typename T>
+int launch_mfma(const PrefillArgs& a, hipStream_t st) {
+  const int hw = gcd_int(a.G, kPfWaves);
+  const int rbw = kPfWaves / hw;
+  const int n_rb = (a.Sq + kPfRows - 1) / kPfRows;
+  const int n_rbg = (n_rb + rbw - 1) / rbw;
+  dim3 grid(n_rbg, a.Hkv * (a.G / hw), a.B);
+  if (a.D <= 64)
+    prefill_mfma_kernel<T, 64><<<grid, 64 * kPfWaves, 0, st>>>(a, hw, n_rbg);
+  else
+    prefill_mfma_kernel<T, 128><<<grid, 64 * kPfWaves, 0, st>>>(a, hw, n_rbg);
+  return lc_check_launch("lc_prefill_attn_fwd (mfma)");
+}
+
 template <typename T>
 int launch_generic(const PrefillArgs& a, hipStream_t st) {
   dim3 grid((a.Sq + 63) / 64, a.Hq, a.B);
@@ -152,13 +420,20 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
   a.q_offset = (int)q_offset;
   a.scale_log2 = scale * kLog2e;
   hipStream_t st = lc_stream(stream);
+  // MFMA path: 16-bit types, D a multiple of 8 up to 128 (padded to 64 or
+  // 128), 16-byte aligned rows.
+  bool mfma = (dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16) && D % 8 == 0 && D <= 128 &&
+              lc_aligned(q, 16) && lc_aligned(k, 16) && lc_aligned(v, 16) && lc_aligned(o, 16);
+  for (int i = 0; i < 3; ++i)
+    mfma = mfma && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 &&
+           o_strides[i] % 8 == 0;
   switch (dtype) {
     case LC_DTYPE_F32:
       return launch_generic<float>(a, st);
     case LC_DTYPE_BF16:
-      return launch_generic<bf16_t>(a, st);
+      return mfma ? launch_mfma<bf16_t>(a, st) : launch_generic<bf16_t>(a, st);
     case LC_DTYPE_F16:
-      return launch_generic<f16_t>(a, st);
+      return mfma ? launch_mfma<f16_t>(a, st) : launch_generic<f16_t>(a, st);
     default:
       return lc_fail(LC_EINVAL, "lc_prefill_attn_fwd: unknown dtype %d", dtype);
   }
