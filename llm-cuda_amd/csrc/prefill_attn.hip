@@ -111,8 +111,9 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 //   index h*8 + jj*4 + i is mapped to key 16jp + 8jj + 4h + i, so each lane's
 //   P^T operand is its own S^T registers (rounded to bf16/f16); V^T operands
 //   come from ds_read_b64_tr_b16 (4 keys x 16 d per 16-lane group).
-// K/V tiles are double-buffered: the next tile's global loads are in flight
-// (registers) while the current tile computes from LDS.
+// K/V tiles are double-buffered in LDS: the next tile is fetched by
+// buffer-to-LDS DMA loads (no register staging) while the current one
+// computes.
 // ---------------------------------------------------------------------------
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
@@ -141,16 +142,19 @@ constexpr int kPfKeys = 64;     // keys per tile
 constexpr float kPfRescaleLog2 = 8.0f;
 
 template <typename T, int DPAD>
-__global__ __launch_bounds__(64 * kPfWaves) void prefill_mfma_kernel(PrefillArgs a, int hw,
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+prefill_mfma_kernel(PrefillArgs a, int hw,
                                                                      int n_rbg) {
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
   constexpr int KS = DPAD / 16;          // QK^T k-steps (16 d each)
   constexpr int DTL = DPAD / 32;         // 32-row d tiles of O^T
-  constexpr int LROW = DPAD + 8;         // LDS row pitch (elements)
-  constexpr int TILE = kPfKeys * LROW;   // elements per K or V tile buffer
   constexpr int CPR = DPAD / 8;          // 16-byte chunks per row
-  constexpr int LPT = kPfKeys * CPR / (64 * kPfWaves);  // 16-byte loads per thread per tensor
+  constexpr int RPI = 64 / CPR;          // rows per 1 KB LDS-DMA instruction
+  constexpr int NIW = kPfKeys / (RPI * kPfWaves);  // instructions per wave per tensor
+  constexpr int TILE = kPfKeys * DPAD;   // elements per K or V tile buffer
+  // LDS tiles are unpadded; 16-byte chunk c of row r sits at position
+  // c ^ (r % CPR), which spreads the 32 rows read at one chunk across banks.
   __shared__ __align__(16) T lds[2][2][TILE];  // [buffer][K, V][tile]
 
   const int tid = threadIdx.x;
@@ -175,11 +179,19 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_mfma_kernel(PrefillArgs
   const T* qbase = static_cast<const T*>(a.q) + b * a.qs[0] + (int64_t)head * a.qs[1];
   const T* kbase = static_cast<const T*>(a.k) + b * a.ks[0] + (int64_t)kvh * a.ks[1];
   const T* vbase = static_cast<const T*>(a.v) + b * a.vs[0] + (int64_t)kvh * a.vs[1];
+  // Buffer descriptors over this (b, kv head)'s K and V rows: loads past the
+  // last key (or past head_dim) are out of range and land in LDS as zeros.
+  const int kbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.ks[2] + a.D) * sizeof(T)) : 0;
+  const int vbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.vs[2] + a.D) * sizeof(T)) : 0;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kbase), 0, kbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vbase), 0, vbytes, 0x00020000);
 
   // Q^T operand registers.
   v8 qop[KS];
+  const int qi = r0 + l32;
   {
-    const int qi = r0 + l32;
     const bool ok = wave_active && qi < a.Sq;
     const T* qrow = qbase + (int64_t)qi * a.qs[2] + hh * (DPAD / 2);
 #pragma unroll
@@ -195,58 +207,54 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_mfma_kernel(PrefillArgs
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
   float m_ref = -INFINITY, l_lane = 0.f;
-  const int qi = r0 + l32;
 
-  // Tile staging: thread tid loads chunks c = tid + 256 * u of the K and V tile.
-  u32x4_t stk[LPT], stv[LPT];
-  auto load_tile = [&](int k0) {
+  // LDS-DMA tile load: instruction u of this wave fills rows
+  // (wave * NIW + u) * RPI .. + RPI - 1; lane l writes row + l / CPR,
+  // position l % CPR, i.e. global chunk (l % CPR) ^ (row % CPR).
+  const int ld_row = lane / CPR;
+  const int ld_pos = lane % CPR;
+  auto load_tile = [&](int k0, int buf) {
 #pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int c = tid + 64 * kPfWaves * u;
-      const int row = c / CPR, ch = c - row * CPR;
+    for (int u = 0; u < NIW; ++u) {
+      const int row0 = (wave * NIW + u) * RPI;
+      const int row = row0 + ld_row;
+      const int ch = ld_pos ^ (row % CPR);
       const int key = k0 + row;
       const bool ok = key < kv_end && ch * 8 < a.D;
-      stk[u] = ok ? *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * a.ks[2] + ch * 8)
-                  : u32x4_t{0, 0, 0, 0};
-      stv[u] = ok ? *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * a.vs[2] + ch * 8)
-                  : u32x4_t{0, 0, 0, 0};
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int c = tid + 64 * kPfWaves * u;
-      const int row = c / CPR, ch = c - row * CPR;
-      *reinterpret_cast<u32x4_t*>(&lds[buf][0][row * LROW + ch * 8]) = stk[u];
-      *reinterpret_cast<u32x4_t*>(&lds[buf][1][row * LROW + ch * 8]) = stv[u];
+      const int koff = ok ? static_cast<int>(((int64_t)key * a.ks[2] + ch * 8) * sizeof(T)) : INT32_MIN;
+      const int voff = ok ? static_cast<int>(((int64_t)key * a.vs[2] + ch * 8) * sizeof(T)) : INT32_MIN;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (LC_LDS void*)(&lds[buf][0][row0 * DPAD]), 16, koff, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (LC_LDS void*)(&lds[buf][1][row0 * DPAD]), 16, voff, 0, 0, 0);
     }
   };
 
   const int n_tiles = (kv_end + kPfKeys - 1) / kPfKeys;
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  if (n_tiles > 0) load_tile(0, 0);
   __syncthreads();
+  const int gq = lane >> 4;
+  const int te = (lane & 15) >> 2, tc = lane & 3;
   for (int it = 0; it < n_tiles; ++it) {
     const int buf = it & 1;
     const int k0 = it * kPfKeys;
-    const bool more = it + 1 < n_tiles;
-    if (more) load_tile(k0 + kPfKeys);
+    if (it + 1 < n_tiles) load_tile(k0 + kPfKeys, buf ^ 1);
 
     if (wave_active && k0 < my_kv_end) {
       const T* kt_lds = &lds[buf][0][0];
-      const T* vt_lds = &lds[buf][1][0];
       // S^T for the two 32-key halves.
       f32x16_t sacc[2];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-        const T* krow = kt_lds + (kt * 32 + l32) * LROW + hh * (DPAD / 2);
+        const int row = kt * 32 + l32;
+        const T* krow = kt_lds + row * DPAD;
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-          sacc[kt] = Ops::mma(*reinterpret_cast<const v8*>(krow + s * 8), qop[s], sacc[kt]);
+        for (int s = 0; s < KS; ++s) {
+          const int pos = (hh * (CPR / 2) + s) ^ (row % CPR);
+          sacc[kt] = Ops::mma(*reinterpret_cast<const v8*>(krow + pos * 8), qop[s], sacc[kt]);
+        }
       }
       // Scale and mask: key k0 + kt*32 + 8j + 4hh + i vs query qi.
       const bool need_mask = k0 + kPfKeys > min(a.Skv, r0 + a.q_offset + 1);
@@ -285,38 +293,33 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_mfma_kernel(PrefillArgs
           l_lane += p;
           pop[kt][r >> 3][r & 7] = static_cast<T>(p);
         }
-      // O^T += V^T P^T. Transposed reads: 16-lane group gq = lane / 16 covers
-      // keys 4hh .. 4hh+3 (+8jj, +16jp, +32kt) and d = dt*32 + (gq & 1)*16 .. +15.
-      const int gq = lane >> 4;
-      const int e = (lane & 15) >> 2, c = lane & 3;
-      LC_LDS const short* vs = (LC_LDS const short*)(vt_lds);
-      const int vrow0 = (hh * 4 + e) * LROW + (gq & 1) * 16 + 4 * c;
+      // O^T += V^T P^T. Transposed reads: 16-lane group gq covers keys
+      // 4hh .. 4hh+3 (+8jj, +16jp, +32kt) and d = dt*32 + (gq & 1)*16 .. +15;
+      // lane 4e + c addresses key +e, d + 4c.
+      LC_LDS const short* vs = (LC_LDS const short*)(&lds[buf][1][0]);
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int jp = 0; jp < 2; ++jp) {
-          const int rbase = vrow0 + (kt * 32 + jp * 16) * LROW;
+        for (int jp = 0; jp < 2; ++jp)
 #pragma unroll
           for (int dt = 0; dt < DTL; ++dt) {
-            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (LC_LDS i16x4_t*)(vs + rbase + dt * 32));
-            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (LC_LDS i16x4_t*)(vs + rbase + 8 * LROW + dt * 32));
+            const int d = dt * 32 + (gq & 1) * 16 + 4 * tc;
+            const int kr0 = kt * 32 + jp * 16 + hh * 4 + te;
+            const int kr1 = kr0 + 8;
+            const int a0 = kr0 * DPAD + (((d >> 3) ^ (kr0 % CPR)) << 3) + (d & 7);
+            const int a1 = kr1 * DPAD + (((d >> 3) ^ (kr1 % CPR)) << 3) + (d & 7);
+            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(vs + a0));
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(vs + a1));
             const i16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
             o[dt] = Ops::mma(__builtin_bit_cast(v8, both), pop[kt][jp], o[dt]);
           }
-        }
     }
-    if (more) {
-      store_tile(buf ^ 1);
-    }
-    __syncthreads();
+    __syncthreads();  // next tile landed (vmcnt) and every wave is done with this one
   }
 
   if (!wave_active) return;
   float l_tot = l_lane + __shfl_xor(l_lane, 32, 64);
-  const bool row_ok = qi < a.Sq;
-  if (!row_ok) return;
+  if (qi >= a.Sq) return;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   T* orow = static_cast<T*>(a.o) + b * a.os[0] + (int64_t)head * a.os[1] + (int64_t)qi * a.os[2];
 #pragma unroll
@@ -422,8 +425,11 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
   hipStream_t st = lc_stream(stream);
   // MFMA path: 16-bit types, D a multiple of 8 up to 128 (padded to 64 or
   // 128), 16-byte aligned rows.
+  const int64_t esz = lc_dtype_size(dtype);
   bool mfma = (dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16) && D % 8 == 0 && D <= 128 &&
-              lc_aligned(q, 16) && lc_aligned(k, 16) && lc_aligned(v, 16) && lc_aligned(o, 16);
+              lc_aligned(q, 16) && lc_aligned(k, 16) && lc_aligned(v, 16) && lc_aligned(o, 16) &&
+              (Skv * k_strides[2] + D) * esz < (1LL << 31) &&
+              (Skv * v_strides[2] + D) * esz < (1LL << 31);
   for (int i = 0; i < 3; ++i)
     mfma = mfma && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 &&
            o_strides[i] % 8 == 0;
