@@ -163,12 +163,22 @@ prefill_mfma_kernel(PrefillArgs a, int hw,
   const int l32 = lane & 31;
   const int hh = lane >> 5;
   const int rbw = kPfWaves / hw;
-  // Heaviest (latest) row groups first: causal work grows with the row index.
-  const int rbg = n_rbg - 1 - (int)blockIdx.x;
   const int n_hg = a.G / hw;
-  const int kvh = blockIdx.y / n_hg;
-  const int hgi = blockIdx.y - kvh * n_hg;
-  const int b = blockIdx.z;
+  // XCD-aware order: the dispatcher deals consecutive workgroups round-robin
+  // to the 8 XCDs (each with its own L2). Work item W = xcd * per_xcd + k is
+  // given to the k-th workgroup landing on XCD xcd, so each XCD walks whole
+  // (b, kv head, head group) units in turn and their K/V stays in its L2.
+  // Within a unit the heaviest (latest) row groups come first.
+  const int nwg = gridDim.x;
+  const int lin = blockIdx.x;
+  int work = lin;
+  if ((nwg & 7) == 0) work = (lin & 7) * (nwg >> 3) + (lin >> 3);
+  const int unit = work / n_rbg;
+  const int rbg = n_rbg - 1 - (work - unit * n_rbg);
+  const int kvh_hg = unit % (a.Hkv * n_hg);
+  const int b = unit / (a.Hkv * n_hg);
+  const int kvh = kvh_hg / n_hg;
+  const int hgi = kvh_hg - kvh * n_hg;
   const int head = kvh * a.G + hgi * hw + (wave % hw);
   const int r0 = (rbg * rbw + wave / hw) * kPfRows;
   const int wg_last_row = min(a.Sq - 1, (rbg * rbw + rbw) * kPfRows - 1);
@@ -258,20 +268,23 @@ prefill_mfma_kernel(PrefillArgs a, int hw,
       }
       // Scale and mask: key k0 + kt*32 + 8j + 4hh + i vs query qi.
       const bool need_mask = k0 + kPfKeys > min(a.Skv, r0 + a.q_offset + 1);
+      // Raw scores are masked and maxed; the scale (> 0) is applied inside
+      // the exponent as one FMA: p = 2^(s * scale_log2 - m).
+      if (need_mask) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+            if (key > qi + a.q_offset || key >= a.Skv) sacc[kt][r] = -INFINITY;
+          }
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = sacc[kt][r] * a.scale_log2;
-          if (need_mask) {
-            const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-            if (key > qi + a.q_offset || key >= a.Skv) v = -INFINITY;
-          }
-          sacc[kt][r] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
       if (__ballot(mx > m_ref + kPfRescaleLog2)) {
         const float m_new = fmaxf(m_ref, mx);
         const float alpha = m_new == -INFINITY ? 1.f : lc_exp2(m_ref - m_new);
@@ -289,7 +302,7 @@ prefill_mfma_kernel(PrefillArgs a, int hw,
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = lc_exp2(sacc[kt][r] - m_use);
+          const float p = lc_exp2(fmaf(sacc[kt][r], a.scale_log2, -m_use));
           l_lane += p;
           pop[kt][r >> 3][r & 7] = static_cast<T>(p);
         }
@@ -355,7 +368,9 @@ int launch_mfma(const PrefillArgs& a, hipStream_t st) {
   const int rbw = kPfWaves / hw;
   const int n_rb = (a.Sq + kPfRows - 1) / kPfRows;
   const int n_rbg = (n_rb + rbw - 1) / rbw;
-  dim3 grid(n_rbg, a.Hkv * (a.G / hw), a.B);
+  const int64_t nwg = (int64_t)n_rbg * a.Hkv * (a.G / hw) * a.B;
+  LC_REQUIRE(nwg < (1LL << 31), "lc_prefill_attn_fwd: grid too large");
+  dim3 grid(static_cast<unsigned>(nwg));
   if (a.D <= 64)
     prefill_mfma_kernel<T, 64><<<grid, 64 * kPfWaves, 0, st>>>(a, hw, n_rbg);
   else
