@@ -230,8 +230,147 @@ def run_prefill(args):
     return result
 
 
+def _model8b_config():
+    from llm_cuda.models.llama3.config import Llama3Config
+
+    return Llama3Config(vocab_size=128256, hidden_size=4096, intermediate_size=14336,
+                        num_hidden_layers=32, num_attention_heads=32, num_key_value_heads=8,
+                        max_position_embeddings=8192)
+
+
 def run_model(args):
-    raise NotImplementedError("model8b workload not implemented yet")
+    """one decode step of random-init Llama-3-8B (bf16), batch 32,
+    paged KV at context 2048 (seeded random page permutation, pools ~N(0,1)).
+
+    The step (embedding, 32 layers of RMSNorm / QKV / RoPE / KV append / paged
+    decode / o_proj / SwiGLU MLP, final norm, lm_head, greedy argmax) is
+    captured once in a HIP graph; the graph starts by resetting every layer's
+    seq_lens to 2048, so each replay decodes position 2048 against the same
+    cache. The first replay is checked against the eager step.
+    """
+    import torch
+
+    from llm_cuda.models.llama3.kv_cache import PagedKVCache
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    dev = torch.device("cuda", 0)
+    cfg = _model8b_config()
+    B, ctx, P = 32, 2048, 64
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Llama3ForCausalLM(cfg)
+    model = model.to(device=dev, dtype=torch.bfloat16).eval()
+    torch.cuda.synchronize()
+    max_pages = math.ceil((ctx + 1) / P)
+    g = torch.Generator().manual_seed(0)
+    table = torch.randperm(B * max_pages, generator=g).to(torch.int32).view(B, max_pages)
+    cache = PagedKVCache.create(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
+                                max_pages * P, P, dev, torch.bfloat16, batch_size=B,
+                                block_table=table, num_pages=B * max_pages)
+    gd = torch.Generator(device=dev).manual_seed(0)
+    for layer in cache.layer_caches:
+        layer.key_pages.normal_(generator=gd)
+        layer.value_pages.normal_(generator=gd)
+    ids = torch.randint(0, cfg.vocab_size, (B, 1), generator=gd, device=dev)
+
+    def reset():
+        for layer in cache.layer_caches:
+            layer.seq_lens.fill_(ctx)
+            layer.lengths = [ctx] * B
+
+    def step():
+        for layer in cache.layer_caches:
+            layer.seq_lens.fill_(ctx)
+        out = model(input_ids=ids, past_key_values=cache, use_cache=True)
+        return torch.argmax(out["logits"][:, -1, :], dim=-1), out["logits"]
+
+    with torch.no_grad():
+        reset()
+        eager_ids, eager_logits = step()
+        eager_logits = eager_logits.float().clone()
+        # warm the allocator on a side stream, then capture
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                reset()
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        reset()
+        with torch.cuda.graph(graph):
+            g_ids, g_logits = step()
+        reset()
+        graph.replay()
+        torch.cuda.synchronize()
+        diff = (g_logits.float() - eager_logits).abs().max().item()
+        if not torch.equal(g_ids, eager_ids) or diff > 1e-2:
+            raise RuntimeError(f"graph replay differs from eager step (max |dlogit| {diff})")
+        ms, wall = time_steps(graph.replay, args.steps, args.warmup)
+    tok_s = B / (ms * 1e-3)
+    weights = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
+    kv = cfg.num_hidden_layers * B * ctx * cfg.num_key_value_heads * cfg.head_dim * 2 * 2
+    gbs = (weights + kv) / (ms * 1e-3) / 1e9
+    log(f"model8b: {ms:.3f} ms/step -> {tok_s:.0f} tok/s; weights {weights / 1e9:.2f} GB + KV "
+        f"{kv / 1e9:.2f} GB per step -> {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+    result = {
+        "metric": METRIC, "value": round(tok_s, 1), "unit": "tok/s", "ms_per_step": round(ms, 5),
+        "dtype": "bf16",
+        "config": {"workload": "Llama-3-8B decode step, random-init bf16 (BASELINE config 4)",
+                   "batch": B, "context": ctx, "page_size": P, "layers": cfg.num_hidden_layers,
+                   "hidden": cfg.hidden_size, "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size,
+                   "hip_graph": True, "bytes_per_step": weights + kv},
+        "roofline": {"bound": "hbm", "kernel": "whole decode step (weights + KV read once)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = _model_cpu_baseline(model, cfg, B, ctx)
+    return result
+
+
+def _model_cpu_baseline(model, cfg, B, ctx):
+    """One decoder layer's decode step in fp32 on the host (oracle pieces), scaled x32
+    layers, plus the lm_head GEMM: the CPU tok/s of the same step."""
+    import torch
+
+    from oracle.decode import decode_attention
+    from oracle.elementwise import apply_rope, build_rope_cache, rms_norm, swiglu
+
+    torch.set_num_threads(cpu_threads())
+    layer = model.model.layers[0]
+    W = {n: p.detach().float().cpu() for n, p in layer.named_parameters()}
+    H, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(B, 1, cfg.hidden_size, generator=g)
+    kc = torch.randn(B, Hkv, ctx + 1, D, generator=g)
+    vc = torch.randn(B, Hkv, ctx + 1, D, generator=g)
+    cos, sin = build_rope_cache(1, D, cfg.rope_theta, torch.float32, position_offset=ctx)
+    lm = model.lm_head.weight.detach().float().cpu()
+
+    def layer_step():
+        h = rms_norm(x, W["input_layernorm.weight"], cfg.rms_norm_eps)
+        q = (h @ W["self_attn.q_proj.weight"].t()).view(B, 1, H, D).transpose(1, 2)
+        k = (h @ W["self_attn.k_proj.weight"].t()).view(B, 1, Hkv, D).transpose(1, 2)
+        v = (h @ W["self_attn.v_proj.weight"].t()).view(B, 1, Hkv, D).transpose(1, 2)
+        q = apply_rope(q, cos, sin)
+        kc[:, :, ctx:] = apply_rope(k, cos, sin)
+        vc[:, :, ctx:] = v
+        o, _ = decode_attention(q, kc, vc)
+        y = x + o.transpose(1, 2).reshape(B, 1, H * D) @ W["self_attn.o_proj.weight"].t()
+        h = rms_norm(y, W["post_attention_layernorm.weight"], cfg.rms_norm_eps)
+        m = swiglu(h @ W["mlp.gate_proj.weight"].t(), h @ W["mlp.up_proj.weight"].t())
+        return y + m @ W["mlp.down_proj.weight"].t()
+
+    t_layer = timed_cpu(layer_step, budget_s=30.0)
+    t_head = timed_cpu(lambda: x[:, -1] @ lm.t(), budget_s=10.0)
+    step_s = t_layer * cfg.num_hidden_layers + t_head
+    return {"value": round(B / step_s, 2), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"layer 0 decode step in fp32 (oracle rms_norm/rope/decode_attention/"
+                      f"swiglu + torch matmuls) {t_layer:.3f} s x {cfg.num_hidden_layers} layers "
+                      f"+ lm_head {t_head:.3f} s"}
 
 
 def decode8b_shape():
