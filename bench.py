@@ -148,12 +148,12 @@ def run_decode(args, shape):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_mfma_kernel + decode_merge_kernel (one decode call)",
+            "kernel": "paged_decode_rows_kernel + decode_merge_kernel (one decode call)",
             "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(f"paged_decode_{shape['name']}"),
         },
     }
     if not args.no_cpu_baseline:
@@ -212,7 +212,8 @@ def run_prefill(args):
                    "rope_theta": 500000.0, "flops_per_step": flops},
         "roofline": {"bound": "mfma", "kernel": "prefill attention", "achieved": round(tflops, 2),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic("prefill_attn_8b")},
     }
     if not args.no_cpu_baseline:
         from oracle.attention import causal_attention
@@ -373,19 +374,53 @@ def _model_cpu_baseline(model, cfg, B, ctx):
                       f"+ lm_head {t_head:.3f} s"}
 
 
+def run_copycal(args):
+    """Plain device copy of a known size (256 MiB bf16 -> 256 MiB): the
+    calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    n = 128 << 20  # elements (256 MiB of bf16)
+    a = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+    b = torch.empty_like(a)
+    ms, _ = time_steps(lambda: b.copy_(a), args.steps, args.warmup)
+    gbs = 2 * n * 2 / (ms * 1e-3) / 1e9
+    log(f"copycal: {ms * 1e3:.1f} us per 256 MiB copy -> {gbs:.0f} GB/s (read + write)")
+    return {"metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 5),
+            "dtype": "bf16", "config": {"workload": "calibration copy, 256 MiB"},
+            "roofline": {"bound": "hbm", "kernel": "torch copy", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": 2 * n * 2}}
+
+
+def measured_traffic(name: str):
+    """HBM bytes per call recorded in profiles/<name>.md (line 'traffic_bytes: N'),
+    from rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by the copy calibration."""
+    path = ROOT / "profiles" / f"{name}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes:"):
+            try:
+                return int(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
 def decode8b_shape():
     import torch
 
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(512, 8193, (64,), generator=g).tolist()
     return {"name": "decode8b", "B": 64, "Hq": 32, "Hkv": 8, "D": 128, "P": 64, "lens": lens,
-            "seed": 0, "cpu_sample": 8,
+            "seed": 0, "cpu_sample": 64,
             "workload": "paged GQA flash-decode, Llama-3-8B shape (BASELINE config 2)"}
 
 
 def decode70b_shape():
     return {"name": "decode70b", "B": 8, "Hq": 64, "Hkv": 8, "D": 128, "P": 64,
-            "lens": [32768] * 8, "seed": 0, "cpu_sample": 1,
+            "lens": [32768] * 8, "seed": 0, "cpu_sample": 8,
             "workload": "long-context paged decode, Llama-3-70B attention shape (BASELINE config 5)"}
 
 
@@ -395,7 +430,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="decode8b",
-                        choices=["decode8b", "decode70b", "prefill", "model8b"])
+                        choices=["decode8b", "decode70b", "prefill", "model8b", "copycal"])
     parser.add_argument("--split-tokens", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     args = parser.parse_args()
@@ -421,6 +456,8 @@ def main() -> int:
         res = run_decode(args, decode70b_shape())
     elif args.workload == "prefill":
         res = run_prefill(args)
+    elif args.workload == "copycal":
+        res = run_copycal(args)
     else:
         res = run_model(args)
     line = {
