@@ -97,6 +97,15 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         ],
         verbose,
     )
+    # A kernel whose host-side launch stub was not emitted links fine but fails
+    # at load time; catch it here.
+    nm = shutil.which("nm")
+    if nm:
+        undef = subprocess.run([nm, "-D", "--undefined-only", str(tmp)], capture_output=True,
+                               text=True).stdout
+        stubs = [ln.split()[-1] for ln in undef.splitlines() if "__device_stub__" in ln]
+        if stubs:
+            raise RuntimeError(f"undefined kernel launch stubs in {tmp.name}: {stubs}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -10,6 +10,8 @@
 // j <= i + q_offset: o = softmax(q.k_j * scale) v, lse = ln-sum-exp.
 #include <math.h>
 
+#include <type_traits>
+
 #include "lc_common.h"
 
 namespace {
@@ -141,10 +143,39 @@ constexpr int kPfRows = 32;     // query rows per wave
 constexpr int kPfKeys = 64;     // keys per tile
 constexpr float kPfRescaleLog2 = 8.0f;
 
+template <int NIW>
+struct PfLoadOffsets {
+  int k[NIW];
+  int v[NIW];
+};
+
+// Buffer-to-LDS DMA of one K and one V tile: instruction u of wave w fills
+// LDS rows (w * NIW + u) * RPI .. + RPI - 1 of buffer BUF.
+template <int NIW, int RPI, int ROW_B, int TILE_B>
+__device__ __forceinline__ void pf_load_tile(const void* kbase, int kbytes, const void* vbase,
+                                             int vbytes, char* lds, int buf, int wave,
+                                             PfLoadOffsets<NIW> off, int kadd, int vadd) {
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(kbase), 0, kbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(vbase), 0, vbytes, 0x00020000);
+#pragma unroll
+  for (int u = 0; u < NIW; ++u) {
+    const int row0 = (wave * NIW + u) * RPI;
+    // (plain local ints: the host pass of hipcc rejects this builtin when its
+    // offset operand is a member of a dependent-type parameter)
+    const int ko = off.k[u] + kadd;
+    const int vo = off.v[u] + vadd;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rk, (LC_LDS void*)(lds + buf * 2 * TILE_B + row0 * ROW_B), 16, ko, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rv, (LC_LDS void*)(lds + buf * 2 * TILE_B + TILE_B + row0 * ROW_B), 16, vo, 0, 0, 0);
+  }
+}
+
 template <typename T, int DPAD>
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void
-prefill_mfma_kernel(PrefillArgs a, int hw,
-                                                                     int n_rbg) {
+prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
   constexpr int KS = DPAD / 16;          // QK^T k-steps (16 d each)
@@ -152,10 +183,12 @@ prefill_mfma_kernel(PrefillArgs a, int hw,
   constexpr int CPR = DPAD / 8;          // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;          // rows per 1 KB LDS-DMA instruction
   constexpr int NIW = kPfKeys / (RPI * kPfWaves);  // instructions per wave per tensor
-  constexpr int TILE = kPfKeys * DPAD;   // elements per K or V tile buffer
-  // LDS tiles are unpadded; 16-byte chunk c of row r sits at position
-  // c ^ (r % CPR), which spreads the 32 rows read at one chunk across banks.
-  __shared__ __align__(16) T lds[2][2][TILE];  // [buffer][K, V][tile]
+  constexpr int TILE_B = kPfKeys * DPAD * (int)sizeof(T);  // bytes per K or V tile
+  constexpr int ROW_B = DPAD * (int)sizeof(T);
+  // LDS: [buffer][K, V] tiles, unpadded; 16-byte chunk c of row r sits at
+  // position c ^ (r % CPR), which spreads the rows read at one chunk across banks.
+  __shared__ __align__(16) char lds_tiles[2 * 2 * TILE_B];
+  char* const lds = lds_tiles;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -184,19 +217,17 @@ prefill_mfma_kernel(PrefillArgs a, int hw,
   const int wg_last_row = min(a.Sq - 1, (rbg * rbw + rbw) * kPfRows - 1);
   const int kv_end = min(a.Skv, wg_last_row + a.q_offset + 1);  // keys any wave needs
   const int my_kv_end = min(a.Skv, min(a.Sq - 1, r0 + kPfRows - 1) + a.q_offset + 1);
+  // Tiles entirely below this key bound are visible to every row of the wave.
+  const int nomask_end = min(a.Skv, r0 + a.q_offset + 1);
   const bool wave_active = r0 < a.Sq;
 
   const T* qbase = static_cast<const T*>(a.q) + b * a.qs[0] + (int64_t)head * a.qs[1];
   const T* kbase = static_cast<const T*>(a.k) + b * a.ks[0] + (int64_t)kvh * a.ks[1];
   const T* vbase = static_cast<const T*>(a.v) + b * a.vs[0] + (int64_t)kvh * a.vs[1];
-  // Buffer descriptors over this (b, kv head)'s K and V rows: loads past the
-  // last key (or past head_dim) are out of range and land in LDS as zeros.
+  // Buffer descriptors over this (b, kv head)'s K and V rows: rows past the
+  // last key are out of range and land in LDS as zeros.
   const int kbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.ks[2] + a.D) * sizeof(T)) : 0;
   const int vbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.vs[2] + a.D) * sizeof(T)) : 0;
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kbase), 0, kbytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vbase), 0, vbytes, 0x00020000);
 
   // Q^T operand registers.
   v8 qop[KS];
@@ -211,6 +242,43 @@ prefill_mfma_kernel(PrefillArgs a, int hw,
     }
   }
 
+  // Loop-invariant per-lane byte offsets.
+  // LDS-DMA loads: instruction u of this wave fills rows (wave*NIW + u)*RPI ..;
+  // lane l writes row + l / CPR at position l % CPR, i.e. global chunk
+  // (l % CPR) ^ (row % CPR) (chunks past head_dim re-read chunk 0: their K
+  // meets zero Q elements and their V lands in discarded output rows).
+  PfLoadOffsets<NIW> ldoff;
+#pragma unroll
+  for (int u = 0; u < NIW; ++u) {
+    const int row = (wave * NIW + u) * RPI + lane / CPR;
+    int ch = (lane % CPR) ^ (row % CPR);
+    ch = ch * 8 < a.D ? ch : 0;
+    ldoff.k[u] = static_cast<int>(((int64_t)row * a.ks[2] + ch * 8) * sizeof(T));
+    ldoff.v[u] = static_cast<int>(((int64_t)row * a.vs[2] + ch * 8) * sizeof(T));
+  }
+  const int kstep_b = static_cast<int>(kPfKeys * a.ks[2] * sizeof(T));
+  const int vstep_b = static_cast<int>(kPfKeys * a.vs[2] * sizeof(T));
+  // K operand reads: row kt*32 + l32, chunk hh*CPR/2 + s (kt is an immediate).
+  int kaddr[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    kaddr[s] = l32 * ROW_B + (((hh * (CPR / 2) + s) ^ (l32 % CPR)) << 4);
+  // V^T transposed reads: 16-lane group gq covers keys 4hh .. 4hh+3 (+8jj,
+  // +16jp, +32kt as immediates) and d = dt*32 + (gq & 1)*16 .. +15; lane
+  // 4e + c addresses key +e, d + 4c.
+  int vaddr[2][DTL];
+  {
+    const int gq = lane >> 4, te = (lane & 15) >> 2, tc = lane & 3;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt) {
+        const int kr = jj * 8 + hh * 4 + te;
+        const int d = dt * 32 + (gq & 1) * 16 + 4 * tc;
+        vaddr[jj][dt] = kr * ROW_B + ((((d >> 3) ^ (kr % CPR)) << 4) | ((d & 7) * (int)sizeof(T)));
+      }
+  }
+
   f32x16_t o[DTL];
 #pragma unroll
   for (int i = 0; i < DTL; ++i)
@@ -218,116 +286,106 @@ prefill_mfma_kernel(PrefillArgs a, int hw,
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
   float m_ref = -INFINITY, l_lane = 0.f;
 
-  // LDS-DMA tile load: instruction u of this wave fills rows
-  // (wave * NIW + u) * RPI .. + RPI - 1; lane l writes row + l / CPR,
-  // position l % CPR, i.e. global chunk (l % CPR) ^ (row % CPR).
-  const int ld_row = lane / CPR;
-  const int ld_pos = lane % CPR;
-  auto load_tile = [&](int k0, int buf) {
-#pragma unroll
-    for (int u = 0; u < NIW; ++u) {
-      const int row0 = (wave * NIW + u) * RPI;
-      const int row = row0 + ld_row;
-      const int ch = ld_pos ^ (row % CPR);
-      const int key = k0 + row;
-      const bool ok = key < kv_end && ch * 8 < a.D;
-      const int koff = ok ? static_cast<int>(((int64_t)key * a.ks[2] + ch * 8) * sizeof(T)) : INT32_MIN;
-      const int voff = ok ? static_cast<int>(((int64_t)key * a.vs[2] + ch * 8) * sizeof(T)) : INT32_MIN;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rk, (LC_LDS void*)(&lds[buf][0][row0 * DPAD]), 16, koff, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rv, (LC_LDS void*)(&lds[buf][1][row0 * DPAD]), 16, voff, 0, 0, 0);
-    }
+  // Buffer index and mask flag are compile-time constants of each call
+  // (std::integral_constant arguments), so LDS offsets fold into instruction
+  // immediates and unmasked tiles carry no mask code.
+  auto load_tile = [&](int tile, auto buf_c) {
+    constexpr int BUF = decltype(buf_c)::value;
+    pf_load_tile<NIW, RPI, ROW_B, TILE_B>(kbase, kbytes, vbase, vbytes, lds, BUF, wave, ldoff,
+                                          tile * kstep_b, tile * vstep_b);
   };
 
-  const int n_tiles = (kv_end + kPfKeys - 1) / kPfKeys;
-  if (n_tiles > 0) load_tile(0, 0);
-  __syncthreads();
-  const int gq = lane >> 4;
-  const int te = (lane & 15) >> 2, tc = lane & 3;
-  for (int it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1;
-    const int k0 = it * kPfKeys;
-    if (it + 1 < n_tiles) load_tile(k0 + kPfKeys, buf ^ 1);
-
-    if (wave_active && k0 < my_kv_end) {
-      const T* kt_lds = &lds[buf][0][0];
-      // S^T for the two 32-key halves.
-      f32x16_t sacc[2];
+  auto compute_tile = [&](int k0, auto buf_c, auto mask_c) {
+    constexpr int BUF = decltype(buf_c)::value;
+    constexpr bool MASK = decltype(mask_c)::value;
+    const char* kt_lds = lds + BUF * 2 * TILE_B;
+    LC_LDS const char* vt_lds = (LC_LDS const char*)(lds + BUF * 2 * TILE_B + TILE_B);
+    f32x16_t sacc[2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-        const int row = kt * 32 + l32;
-        const T* krow = kt_lds + row * DPAD;
+      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const int pos = (hh * (CPR / 2) + s) ^ (row % CPR);
-          sacc[kt] = Ops::mma(*reinterpret_cast<const v8*>(krow + pos * 8), qop[s], sacc[kt]);
-        }
-      }
-      // Scale and mask: key k0 + kt*32 + 8j + 4hh + i vs query qi.
-      const bool need_mask = k0 + kPfKeys > min(a.Skv, r0 + a.q_offset + 1);
-      // Raw scores are masked and maxed; the scale (> 0) is applied inside
-      // the exponent as one FMA: p = 2^(s * scale_log2 - m).
-      if (need_mask) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-            if (key > qi + a.q_offset || key >= a.Skv) sacc[kt][r] = -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
-      if (__ballot(mx > m_ref + kPfRescaleLog2)) {
-        const float m_new = fmaxf(m_ref, mx);
-        const float alpha = m_new == -INFINITY ? 1.f : lc_exp2(m_ref - m_new);
-        l_lane *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DTL; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-        m_ref = m_new;
-      }
-      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-      // P^T operands: step (kt, jp) takes accumulator rows j = 2jp, 2jp + 1.
-      v8 pop[2][2];
+      for (int s = 0; s < KS; ++s)
+        sacc[kt] = Ops::mma(*reinterpret_cast<const v8*>(kt_lds + kaddr[s] + kt * 32 * ROW_B),
+                            qop[s], sacc[kt]);
+    }
+    if constexpr (MASK) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = lc_exp2(fmaf(sacc[kt][r], a.scale_log2, -m_use));
-          l_lane += p;
-          pop[kt][r >> 3][r & 7] = static_cast<T>(p);
+          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+          if (key > qi + a.q_offset || key >= a.Skv) sacc[kt][r] = -INFINITY;
         }
-      // O^T += V^T P^T. Transposed reads: 16-lane group gq covers keys
-      // 4hh .. 4hh+3 (+8jj, +16jp, +32kt) and d = dt*32 + (gq & 1)*16 .. +15;
-      // lane 4e + c addresses key +e, d + 4c.
-      LC_LDS const short* vs = (LC_LDS const short*)(&lds[buf][1][0]);
+    }
+    // Raw scores are maxed; the scale (> 0) is applied inside the exponent as
+    // one FMA: p = 2^(s * scale_log2 - m).
+    float mx = -INFINITY;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int jp = 0; jp < 2; ++jp)
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+    // Rare (a few times per row): keep it a real branch rather than letting
+    // the compiler turn it into 64 unconditional multiplies per tile.
+    if (__builtin_expect(__ballot(mx > m_ref + kPfRescaleLog2) != 0, 0)) {
+      const float m_new = fmaxf(m_ref, mx);
+      const float alpha = m_new == -INFINITY ? 1.f : lc_exp2(m_ref - m_new);
+      l_lane *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < DTL; ++dt) {
-            const int d = dt * 32 + (gq & 1) * 16 + 4 * tc;
-            const int kr0 = kt * 32 + jp * 16 + hh * 4 + te;
-            const int kr1 = kr0 + 8;
-            const int a0 = kr0 * DPAD + (((d >> 3) ^ (kr0 % CPR)) << 3) + (d & 7);
-            const int a1 = kr1 * DPAD + (((d >> 3) ^ (kr1 % CPR)) << 3) + (d & 7);
-            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(vs + a0));
-            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(vs + a1));
-            const i16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            o[dt] = Ops::mma(__builtin_bit_cast(v8, both), pop[kt][jp], o[dt]);
-          }
+      for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      m_ref = m_new;
+    }
+    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+    // P^T operands: step (kt, jp) takes accumulator rows j = 2jp, 2jp + 1.
+    v8 pop[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = lc_exp2(fmaf(sacc[kt][r], a.scale_log2, -m_use));
+        l_lane += p;
+        pop[kt][r >> 3][r & 7] = static_cast<T>(p);
+      }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt) {
+          const int rowoff = (kt * 32 + jp * 16) * ROW_B;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(vt_lds + vaddr[0][dt] + rowoff));
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(vt_lds + vaddr[1][dt] + rowoff));
+          const i16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          o[dt] = Ops::mma(__builtin_bit_cast(v8, both), pop[kt][jp], o[dt]);
+        }
+  };
+
+  auto step = [&](int it, int n_tiles, auto buf_c) {
+    constexpr int BUF = decltype(buf_c)::value;
+    if (it + 1 < n_tiles) load_tile(it + 1, std::integral_constant<int, BUF ^ 1>{});
+    const int k0 = it * kPfKeys;
+    if (wave_active && k0 < my_kv_end) {
+      if (k0 + kPfKeys <= nomask_end)
+        compute_tile(k0, buf_c, std::false_type{});
+      else
+        compute_tile(k0, buf_c, std::true_type{});
     }
     __syncthreads();  // next tile landed (vmcnt) and every wave is done with this one
+  };
+
+  const int n_tiles = (kv_end + kPfKeys - 1) / kPfKeys;
+  if (n_tiles > 0) load_tile(0, std::integral_constant<int, 0>{});
+  __syncthreads();
+  for (int it = 0; it < n_tiles; it += 2) {
+    step(it, n_tiles, std::integral_constant<int, 0>{});
+    if (it + 1 >= n_tiles) break;
+    step(it + 1, n_tiles, std::integral_constant<int, 1>{});
   }
 
   if (!wave_active) return;
