@@ -100,7 +100,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 // Workgroup = 4 waves that share one kv head: wave w computes 32 query rows of
 // one q head. The workgroup covers HW = gcd(G, 4) heads of the kv group times
 // 4 / HW blocks of 32 rows (G = 4: the group's 4 heads on the same rows), so
-// every K/V tile staged in LDS feeds 4 waves.
+// every K/V tile staged in LDS feeds 4 waves. Two workgroups share a CU.
 //
 // Per 64-key tile and wave:
 //   S^T[32 keys x 32 q] = K[32 keys x 16 d] * Q^T[16 d x 32 q], D/16 k-steps
@@ -108,14 +108,25 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 //   registers (lane: query row l % 32, d = (l / 32) * D/2 + 8s .. +8); K
 //   operands are ds_read_b128 of K rows in the same d order.
 //   Keys land on accumulator rows (8j + 4h + i, h = l / 32) and queries on
-//   lanes, so a query's max/sum over keys is 16 in-lane values + 1 shuffle.
+//   lanes, so a query's max/sum over keys is 16 in-lane values + 1 swap.
 //   O^T[32 d x 32 q] += V^T[32 d x 16 keys] * P^T[16 keys x 32 q]: the MFMA k
 //   index h*8 + jj*4 + i is mapped to key 16jp + 8jj + 4h + i, so each lane's
 //   P^T operand is its own S^T registers (rounded to bf16/f16); V^T operands
 //   come from ds_read_b64_tr_b16 (4 keys x 16 d per 16-lane group).
-// K/V tiles are double-buffered in LDS: the next tile is fetched by
-// buffer-to-LDS DMA loads (no register staging) while the current one
-// computes.
+//
+// Software pipeline. The softmax of a tile is split in two halves:
+//   SM1(t): mask, row max, running-max update, x = s * scale_log2 - m;
+//   SM2(t): p = 2^x, row sum, P rounded to the MFMA type.
+// Iteration t interleaves, in one instruction stream,
+//   part A: QK^T of tile t+1 (MFMA) with SM2(t) (VALU);
+//   part B: P(t) V(t) (MFMA) with SM1(t+1) (VALU),
+// so the matrix cores and the VALU of one wave work side by side. A rescale
+// of O (rare: the running max grew by more than 2^8) is applied after part B.
+// LDS holds two K and two V tile buffers as separate arrays. Iteration t reads
+// K(t+1), V(t) and fetches K(t+2), V(t+1) by buffer-to-LDS DMA into the other
+// two; one barrier per iteration publishes them. Reads and DMA targets are
+// distinct LDS objects, so the compiler does not make the reads wait for the
+// DMA in flight.
 // ---------------------------------------------------------------------------
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
@@ -143,34 +154,68 @@ constexpr int kPfRows = 32;     // query rows per wave
 constexpr int kPfKeys = 64;     // keys per tile
 constexpr float kPfRescaleLog2 = 8.0f;
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4],
+// lgkmcnt [11:8]).
+constexpr int kWaitVm0Lgkm0 = 0x0070;  // vmcnt(0) lgkmcnt(0)
+constexpr int kWaitLgkm0 = 0xC07F;     // lgkmcnt(0)
+
+// Workgroup barrier: this wave's LDS reads (and, with WAIT_VM, its DMA) have
+// completed before it arrives.
+template <bool WAIT_VM>
+__device__ __forceinline__ void pf_barrier() {
+  __builtin_amdgcn_s_waitcnt(WAIT_VM ? kWaitVm0Lgkm0 : kWaitLgkm0);
+  lc_compiler_fence();
+  __builtin_amdgcn_s_barrier();
+  lc_compiler_fence();
+}
+
+// LDS swizzle of the prefill K/V tiles: 16-byte chunk c of row r is stored at
+// position c ^ pf_swz(r). Two read patterns must both be bank-conflict free:
+//  * QK^T operands: 16 lanes read one chunk of 16 consecutive rows, so
+//    pf_swz must be a bijection on r mod (rows per bank cycle);
+//  * transposed V^T reads: a 16-lane group reads 4 consecutive rows x 4
+//    consecutive chunks, so 4 consecutive rows must differ in the high
+//    position bits.
+// A plain XOR with r mod 16 fails the second (4 rows map onto the same 4
+// positions); swapping the two 2-bit halves of r mod 16 satisfies both.
+template <int CPR>
+__device__ __forceinline__ int pf_swz(int r) {
+  if constexpr (CPR == 16) {
+    return ((r & 3) << 2) | ((r >> 2) & 3);  // 256-byte rows: one row per bank cycle
+  } else {
+    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);  // 128-byte rows: 2 rows per cycle
+  }
+}
+
 template <int NIW>
 struct PfLoadOffsets {
-  int k[NIW];
-  int v[NIW];
+  int o[NIW];
 };
 
-// Buffer-to-LDS DMA of one K and one V tile: instruction u of wave w fills
-// LDS rows (w * NIW + u) * RPI .. + RPI - 1 of buffer BUF.
-template <int NIW, int RPI, int ROW_B, int TILE_B>
-__device__ __forceinline__ void pf_load_tile(const void* kbase, int kbytes, const void* vbase,
-                                             int vbytes, char* lds, int buf, int wave,
-                                             PfLoadOffsets<NIW> off, int kadd, int vadd) {
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(kbase), 0, kbytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(vbase), 0, vbytes, 0x00020000);
+// Buffer-to-LDS DMA of one 64-row K or V tile: instruction u of wave w fills
+// LDS rows (w * NIW + u) * RPI .. + RPI - 1 of dst.
+template <int NIW, int RPI, int ROW_B>
+__device__ __forceinline__ void pf_dma_tile(const void* base, int nbytes, LC_LDS char* dst,
+                                            int wave, PfLoadOffsets<NIW> off, int add) {
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
 #pragma unroll
   for (int u = 0; u < NIW; ++u) {
     const int row0 = (wave * NIW + u) * RPI;
-    // (plain local ints: the host pass of hipcc rejects this builtin when its
+    // (a plain local int: the host pass of hipcc rejects this builtin when its
     // offset operand is a member of a dependent-type parameter)
-    const int ko = off.k[u] + kadd;
-    const int vo = off.v[u] + vadd;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rk, (LC_LDS void*)(lds + buf * 2 * TILE_B + row0 * ROW_B), 16, ko, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rv, (LC_LDS void*)(lds + buf * 2 * TILE_B + TILE_B + row0 * ROW_B), 16, vo, 0, 0, 0);
+    const int vo = off.o[u];
+    // per-lane offset in voffset, the wave-uniform tile offset in soffset
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LC_LDS void*)(dst + row0 * ROW_B), 16, vo, add,
+                                             0, 0);
   }
+}
+
+// Maximum of x over the two 32-lane halves of the wave (v_permlane32_swap).
+__device__ __forceinline__ float pf_half_max(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
 }
 
 template <typename T, int DPAD>
@@ -182,17 +227,22 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   constexpr int DTL = DPAD / 32;         // 32-row d tiles of O^T
   constexpr int CPR = DPAD / 8;          // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;          // rows per 1 KB LDS-DMA instruction
-  constexpr int NIW = kPfKeys / (RPI * kPfWaves);  // instructions per wave per tensor
+  constexpr int NIW = kPfKeys / (RPI * kPfWaves);  // DMA instructions per wave per tile
   constexpr int TILE_B = kPfKeys * DPAD * (int)sizeof(T);  // bytes per K or V tile
   constexpr int ROW_B = DPAD * (int)sizeof(T);
-  // LDS: [buffer][K, V] tiles, unpadded; 16-byte chunk c of row r sits at
-  // position c ^ (r % CPR), which spreads the rows read at one chunk across banks.
-  __shared__ __align__(16) char lds_tiles[2 * 2 * TILE_B];
-  char* const lds = lds_tiles;
+  // K and V tile buffers (unpadded, chunks swizzled by pf_swz).
+  __shared__ __align__(16) char lds_k0[TILE_B];
+  __shared__ __align__(16) char lds_k1[TILE_B];
+  __shared__ __align__(16) char lds_v0[TILE_B];
+  __shared__ __align__(16) char lds_v1[TILE_B];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  // Scalar copy for the DMA destinations (M0). Control flow keeps using the
+  // vector copy: with every bound provably uniform the optimizer unswitches
+  // the tile loop into many copies and the register allocation breaks down.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int l32 = lane & 31;
   const int hh = lane >> 5;
   const int rbw = kPfWaves / hw;
@@ -245,16 +295,16 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   // Loop-invariant per-lane byte offsets.
   // LDS-DMA loads: instruction u of this wave fills rows (wave*NIW + u)*RPI ..;
   // lane l writes row + l / CPR at position l % CPR, i.e. global chunk
-  // (l % CPR) ^ (row % CPR) (chunks past head_dim re-read chunk 0: their K
+  // (l % CPR) ^ pf_swz(row) (chunks past head_dim re-read chunk 0: their K
   // meets zero Q elements and their V lands in discarded output rows).
-  PfLoadOffsets<NIW> ldoff;
+  PfLoadOffsets<NIW> koff, voff;
 #pragma unroll
   for (int u = 0; u < NIW; ++u) {
     const int row = (wave * NIW + u) * RPI + lane / CPR;
-    int ch = (lane % CPR) ^ (row % CPR);
+    int ch = (lane % CPR) ^ pf_swz<CPR>(row);
     ch = ch * 8 < a.D ? ch : 0;
-    ldoff.k[u] = static_cast<int>(((int64_t)row * a.ks[2] + ch * 8) * sizeof(T));
-    ldoff.v[u] = static_cast<int>(((int64_t)row * a.vs[2] + ch * 8) * sizeof(T));
+    koff.o[u] = static_cast<int>(((int64_t)row * a.ks[2] + ch * 8) * sizeof(T));
+    voff.o[u] = static_cast<int>(((int64_t)row * a.vs[2] + ch * 8) * sizeof(T));
   }
   const int kstep_b = static_cast<int>(kPfKeys * a.ks[2] * sizeof(T));
   const int vstep_b = static_cast<int>(kPfKeys * a.vs[2] * sizeof(T));
@@ -262,7 +312,7 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   int kaddr[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s)
-    kaddr[s] = l32 * ROW_B + (((hh * (CPR / 2) + s) ^ (l32 % CPR)) << 4);
+    kaddr[s] = l32 * ROW_B + (((hh * (CPR / 2) + s) ^ pf_swz<CPR>(l32)) << 4);
   // V^T transposed reads: 16-lane group gq covers keys 4hh .. 4hh+3 (+8jj,
   // +16jp, +32kt as immediates) and d = dt*32 + (gq & 1)*16 .. +15; lane
   // 4e + c addresses key +e, d + 4c.
@@ -275,7 +325,7 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
       for (int dt = 0; dt < DTL; ++dt) {
         const int kr = jj * 8 + hh * 4 + te;
         const int d = dt * 32 + (gq & 1) * 16 + 4 * tc;
-        vaddr[jj][dt] = kr * ROW_B + ((((d >> 3) ^ (kr % CPR)) << 4) | ((d & 7) * (int)sizeof(T)));
+        vaddr[jj][dt] = kr * ROW_B + ((((d >> 3) ^ pf_swz<CPR>(kr)) << 4) | ((d & 7) * (int)sizeof(T)));
       }
   }
 
@@ -285,71 +335,39 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
   float m_ref = -INFINITY, l_lane = 0.f;
+  f32x16_t snx[2];  // raw S^T of the next tile (QK^T output)
+  f32x16_t xcu[2];  // exponents of the current tile (SM1 output)
+  v8 pop[2][2];     // P^T operands of the current tile (SM2 output)
+  float alpha = 1.f;
+  bool rescale = false;
+  const int n_tiles = (kv_end + kPfKeys - 1) / kPfKeys;
 
-  // Buffer index and mask flag are compile-time constants of each call
-  // (std::integral_constant arguments), so LDS offsets fold into instruction
-  // immediates and unmasked tiles carry no mask code.
-  auto load_tile = [&](int tile, auto buf_c) {
-    constexpr int BUF = decltype(buf_c)::value;
-    pf_load_tile<NIW, RPI, ROW_B, TILE_B>(kbase, kbytes, vbase, vbytes, lds, BUF, wave, ldoff,
-                                          tile * kstep_b, tile * vstep_b);
+  auto kbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS char* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS char*)lds_k0;
+    else return (LC_LDS char*)lds_k1;
+  };
+  auto vbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS char* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS char*)lds_v0;
+    else return (LC_LDS char*)lds_v1;
+  };
+  auto live = [&](int t) __attribute__((always_inline)) {
+    return wave_active && t < n_tiles && t * kPfKeys < my_kv_end;
   };
 
-  auto compute_tile = [&](int k0, auto buf_c, auto mask_c) {
-    constexpr int BUF = decltype(buf_c)::value;
-    constexpr bool MASK = decltype(mask_c)::value;
-    const char* kt_lds = lds + BUF * 2 * TILE_B;
-    LC_LDS const char* vt_lds = (LC_LDS const char*)(lds + BUF * 2 * TILE_B + TILE_B);
-    f32x16_t sacc[2];
+  auto qk = [&](LC_LDS const char* kt_lds) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+      for (int r = 0; r < 16; ++r) snx[kt][r] = 0.f;
+    // The two 32-key halves alternate, so consecutive MFMAs are independent.
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        sacc[kt] = Ops::mma(*reinterpret_cast<const v8*>(kt_lds + kaddr[s] + kt * 32 * ROW_B),
-                            qop[s], sacc[kt]);
-    }
-    if constexpr (MASK) {
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-          if (key > qi + a.q_offset || key >= a.Skv) sacc[kt][r] = -INFINITY;
-        }
-    }
-    // Raw scores are maxed; the scale (> 0) is applied inside the exponent as
-    // one FMA: p = 2^(s * scale_log2 - m).
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
-    // Rare (a few times per row): keep it a real branch rather than letting
-    // the compiler turn it into 64 unconditional multiplies per tile.
-    if (__builtin_expect(__ballot(mx > m_ref + kPfRescaleLog2) != 0, 0)) {
-      const float m_new = fmaxf(m_ref, mx);
-      const float alpha = m_new == -INFINITY ? 1.f : lc_exp2(m_ref - m_new);
-      l_lane *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DTL; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-      m_ref = m_new;
-    }
-    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-    // P^T operands: step (kt, jp) takes accumulator rows j = 2jp, 2jp + 1.
-    v8 pop[2][2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = lc_exp2(fmaf(sacc[kt][r], a.scale_log2, -m_use));
-        l_lane += p;
-        pop[kt][r >> 3][r & 7] = static_cast<T>(p);
-      }
+        snx[kt] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(kt_lds + kaddr[s] + kt * 32 * ROW_B),
+                           qop[s], snx[kt]);
+  };
+  auto pv = [&](LC_LDS const char* vt_lds) __attribute__((always_inline)) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -365,27 +383,145 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
           o[dt] = Ops::mma(__builtin_bit_cast(v8, both), pop[kt][jp], o[dt]);
         }
   };
-
-  auto step = [&](int it, int n_tiles, auto buf_c) {
-    constexpr int BUF = decltype(buf_c)::value;
-    if (it + 1 < n_tiles) load_tile(it + 1, std::integral_constant<int, BUF ^ 1>{});
-    const int k0 = it * kPfKeys;
-    if (wave_active && k0 < my_kv_end) {
-      if (k0 + kPfKeys <= nomask_end)
-        compute_tile(k0, buf_c, std::false_type{});
-      else
-        compute_tile(k0, buf_c, std::true_type{});
+  // SM1 of the tile whose raw scores are in snx (keys k0 ..): sets xcu, the
+  // running max and row sum; a required rescale of O is left to apply_rescale.
+  auto sm1 = [&](int k0, auto mask_c) __attribute__((always_inline)) {
+    if constexpr (decltype(mask_c)::value) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+          if (key > qi + a.q_offset || key >= a.Skv) snx[kt][r] = -INFINITY;
+        }
     }
-    __syncthreads();  // next tile landed (vmcnt) and every wave is done with this one
+    // Raw scores are maxed; the scale (> 0) is applied with the shift.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, snx[kt][r]);
+    mx = pf_half_max(mx) * a.scale_log2;
+    // The reference max only moves when some row's max grew by more than 2^8
+    // (exact: O and l always share it).
+    rescale = __ballot(mx > m_ref + kPfRescaleLog2) != 0;
+    const float m_new = rescale ? fmaxf(m_ref, mx) : m_ref;
+    alpha = m_new == -INFINITY ? 1.f : lc_exp2(m_ref - m_new);
+    l_lane *= alpha;
+    m_ref = m_new;
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xcu[kt][r] = fmaf(snx[kt][r], a.scale_log2, -m_use);
+  };
+  auto sm2 = [&]() __attribute__((always_inline)) {
+    // P^T operands: step (kt, jp) takes accumulator rows j = 2jp, 2jp + 1.
+    // The row sum stays in fp32 (a sum of rounded P would cost the lse up to
+    // 2^-9 relative when one key dominates).
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = lc_exp2(xcu[kt][r]);
+        l_lane += p;
+        pop[kt][r >> 3][r & 7] = static_cast<T>(p);
+      }
+  };
+  auto apply_rescale = [&]() __attribute__((always_inline)) {
+    if (__builtin_expect(rescale, 0)) {
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      rescale = false;
+    }
   };
 
-  const int n_tiles = (kv_end + kPfKeys - 1) / kPfKeys;
-  if (n_tiles > 0) load_tile(0, std::integral_constant<int, 0>{});
-  __syncthreads();
-  for (int it = 0; it < n_tiles; it += 2) {
-    step(it, n_tiles, std::integral_constant<int, 0>{});
-    if (it + 1 >= n_tiles) break;
-    step(it + 1, n_tiles, std::integral_constant<int, 1>{});
+  // Iteration t (PAR = t & 1): reads K(t+1) from K buffer PAR ^ 1 and V(t)
+  // from V buffer PAR; fetches K(t+2) -> K buffer PAR, V(t+1) -> V buffer
+  // PAR ^ 1. MASK: tile t+1 needs the causal / key-range mask.
+  auto iteration = [&](int t, auto par_c, auto mask_c) __attribute__((always_inline)) {
+    constexpr int PAR = decltype(par_c)::value;
+    constexpr auto other = std::integral_constant<int, PAR ^ 1>{};
+    if (t + 2 < n_tiles)
+      pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(par_c), wave_s, koff, (t + 2) * kstep_b);
+    if (t + 1 < n_tiles)
+      pf_dma_tile<NIW, RPI, ROW_B>(vbase, vbytes, vbuf(other), wave_s, voff, (t + 1) * vstep_b);
+    const int k1 = (t + 1) * kPfKeys;
+    const bool cur = live(t), nxt = live(t + 1);
+    if (cur && nxt) {
+      qk(kbuf(other));
+      sm2();
+      pv(vbuf(par_c));
+      sm1(k1, mask_c);
+      // Part A: 16 QK^T MFMAs, each followed by one K read 4 MFMAs ahead and
+      // SM2 VALU work; part B: 16 PV MFMAs, each with two V^T reads ahead
+      // and SM1 VALU work.
+      constexpr int NQ = 2 * KS, NP = 4 * DTL, LA = 4;
+      __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
+#pragma unroll
+      for (int j = 0; j < NQ + NP; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        const int nx = j + LA;
+        if (nx < NQ)
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        else if (nx < NQ + NP)
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+    } else {
+      if (nxt) qk(kbuf(other));
+      if (cur) {
+        sm2();
+        pv(vbuf(par_c));
+      }
+      if (nxt) sm1(k1, mask_c);
+    }
+    apply_rescale();
+    pf_barrier<true>();  // this wave's DMA landed, every wave done with K(t+1), V(t)
+  };
+
+  // Prologue: K(0), V(0), K(1) in LDS; S(0) through SM1.
+  if (n_tiles > 0) {
+    pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(std::integral_constant<int, 0>{}), wave_s,
+                                 koff, 0);
+    pf_dma_tile<NIW, RPI, ROW_B>(vbase, vbytes, vbuf(std::integral_constant<int, 0>{}), wave_s,
+                                 voff, 0);
+    if (n_tiles > 1)
+      pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(std::integral_constant<int, 1>{}), wave_s,
+                                   koff, kstep_b);
+  }
+  pf_barrier<true>();
+  if (live(0)) {
+    qk(kbuf(std::integral_constant<int, 0>{}));
+    sm1(0, std::true_type{});
+    rescale = false;  // O is still zero
+  }
+  pf_barrier<false>();  // K buffer 0 is refilled in iteration 0
+  // Iterations whose next tile needs no mask, then the rest (the diagonal
+  // band); two loops rather than a branch per iteration, so each loop body
+  // is a single straight-line interleaved block.
+  const int t_mask = min(n_tiles, max(0, nomask_end / kPfKeys - 1));
+  const std::integral_constant<int, 0> p0{};
+  const std::integral_constant<int, 1> p1{};
+  int t = 0;
+  for (; t + 1 < t_mask; t += 2) {
+    iteration(t, p0, std::false_type{});
+    iteration(t + 1, p1, std::false_type{});
+  }
+  if (t < t_mask) {
+    iteration(t, p0, std::false_type{});
+    ++t;
+    if (t < n_tiles) {
+      iteration(t, p1, std::true_type{});
+      ++t;
+    }
+  }
+  for (; t < n_tiles; t += 2) {
+    iteration(t, p0, std::true_type{});
+    if (t + 1 >= n_tiles) break;
+    iteration(t + 1, p1, std::true_type{});
   }
 
   if (!wave_active) return;
