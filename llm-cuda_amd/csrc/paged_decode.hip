@@ -234,10 +234,10 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   __shared__ __align__(16) T lds_v[kStep * LROW];
 
   const int lane = threadIdx.x;
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y / a.n_hgroups;
-  const int hg = blockIdx.y - kvh * a.n_hgroups;
-  const int b = blockIdx.z;
+  const int split = blockIdx.z;
+  const int kvh = blockIdx.x / a.n_hgroups;
+  const int hg = blockIdx.x - kvh * a.n_hgroups;
+  const int b = blockIdx.y;
   const int len = seq_len_of(a, b);
   const int t_begin = split * a.split_tokens;
   if (t_begin >= len) return;
@@ -353,10 +353,10 @@ __global__ __launch_bounds__(64) void paged_decode_lanes_kernel(DecodeArgs a) {
   __shared__ __align__(16) T lds_v[kStep * LROW];
 
   const int lane = threadIdx.x;
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y / a.n_hgroups;
-  const int hg = blockIdx.y - kvh * a.n_hgroups;
-  const int b = blockIdx.z;
+  const int split = blockIdx.z;
+  const int kvh = blockIdx.x / a.n_hgroups;
+  const int hg = blockIdx.x - kvh * a.n_hgroups;
+  const int b = blockIdx.y;
   const int len = seq_len_of(a, b);
   const int t_begin = split * a.split_tokens;
   if (t_begin >= len) return;
@@ -536,7 +536,11 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, T* __res
 
 template <typename T, int DPAD>
 int launch_mfma(const DecodeArgs& a, bool rows, hipStream_t st) {
-  dim3 grid(a.max_splits, a.Hkv * a.n_hgroups, a.B);
+  // Split-major dispatch order (blockIdx.z = split): workgroups are handed
+  // out in block-id order as earlier ones finish, so the last to start are
+  // the final, mostly partial splits of the longest sequences rather than
+  // full splits of the last sequences, which shortens the ragged tail.
+  dim3 grid(a.Hkv * a.n_hgroups, a.B, a.max_splits);
   if (rows)
     paged_decode_rows_kernel<T, DPAD><<<grid, 64, 0, st>>>(a);
   else
@@ -616,6 +620,8 @@ int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* k
   LC_REQUIRE(bt_stride >= max_pages_per_seq, "lc_paged_decode_fwd: bt_stride < row length");
   LC_REQUIRE(split_tokens > 0 && split_tokens % 64 == 0,
              "lc_paged_decode_fwd: split_tokens must be a positive multiple of 64");
+  LC_REQUIRE(max_splits <= 65535, "lc_paged_decode_fwd: max_splits %lld > 65535",
+             (long long)max_splits);
   LC_REQUIRE(max_splits > 0 && max_splits * split_tokens >= max_pages_per_seq * page_size,
              "lc_paged_decode_fwd: max_splits * split_tokens must cover the block-table "
              "capacity (%lld tokens)",
