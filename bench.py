@@ -7,7 +7,9 @@ step = one paged_decode_attention call (split-K kernel + merge) over all 64
 sequences, inputs resident in HBM. `value` = algorithmic bytes / step time.
 
 Other workloads (--workload): decode70b (config 5), prefill (config 3,
-TFLOP/s), model8b (config 4, tok/s of a full 8B decode step).
+TFLOP/s), model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
+swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
+(counter calibration copy).
 
 Prints one JSON line with the driver's fields plus `roofline` (the dominant
 kernel against MI355X peaks) and `cpu_baseline` (the CPU oracle on the host
@@ -374,6 +376,98 @@ def _model_cpu_baseline(model, cfg, B, ctx):
                       f"+ lm_head {t_head:.3f} s"}
 
 
+def run_elementwise(args, kind: str):
+    """Bandwidth shapes of the fused elementwise kernels (the evidence shapes of
+    the attention path's neighbours): RMSNorm x [16384, 4096], SwiGLU g, u
+    [16384, 14336], RoPE on strided Q [4, 32, 4096, 128] + K [4, 8, 4096, 128]
+    projection views. Inputs are rotated over enough buffers that each step's
+    working set exceeds the 256 MB Infinity Cache; value = algorithmic bytes
+    (inputs read once, outputs written once) / step time."""
+    import torch
+
+    from llm_cuda.kernels import _ops
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    if kind == "rmsnorm":
+        rows, hidden, nbuf = 16384, 4096, 4
+        xs = [torch.randn(rows, hidden, generator=g, device=dev, dtype=bf) for _ in range(nbuf)]
+        w = (1.0 + 0.1 * torch.randn(hidden, generator=g, device=dev)).to(bf)
+        nbytes = 2 * rows * hidden * 2 + hidden * 2
+        calls = [lambda x=x: _ops.rms_norm(x, w, 1e-5) for x in xs]
+        shape = {"x": [rows, hidden], "eps": 1e-5, "buffers_rotated": nbuf}
+        label = "rmsnorm_kernel"
+    elif kind == "swiglu":
+        rows, cols, nbuf = 16384, 14336, 1
+        gs = [torch.randn(rows, cols, generator=g, device=dev, dtype=bf) for _ in range(nbuf)]
+        us = [torch.randn(rows, cols, generator=g, device=dev, dtype=bf) for _ in range(nbuf)]
+        nbytes = 3 * rows * cols * 2
+        calls = [lambda a=a, b=b: _ops.swiglu(a, b) for a, b in zip(gs, us)]
+        shape = {"gate": [rows, cols], "up": [rows, cols], "buffers_rotated": nbuf}
+        label = "swiglu_kernel"
+    else:
+        from llm_cuda.models.llama3.rotary import build_rope_cache
+
+        B, Hq, Hkv, S, D, nbuf = 4, 32, 8, 4096, 128, 2
+        cos, sin = build_rope_cache(S, D, 500000.0, dev, bf)
+        pairs = []
+        for _ in range(nbuf):
+            qp = torch.randn(B, S, Hq * D, generator=g, device=dev, dtype=bf)
+            kp = torch.randn(B, S, Hkv * D, generator=g, device=dev, dtype=bf)
+            pairs.append((qp.view(B, S, Hq, D).transpose(1, 2), kp.view(B, S, Hkv, D).transpose(1, 2)))
+        nbytes = 2 * (B * Hq * S * D + B * Hkv * S * D) * 2 + 2 * S * D * 2
+        calls = [lambda q=q, k=k: _ops.rope(q, cos, sin, k) for q, k in pairs]
+        shape = {"q": [B, Hq, S, D], "k": [B, Hkv, S, D], "layout": "strided projection views",
+                 "rope_theta": 500000.0, "buffers_rotated": nbuf}
+        label = "rope_kernel"
+    state = {"i": 0, "keep": []}
+
+    def step():
+        # the last few outputs stay alive, so outputs rotate over distinct
+        # blocks too and cannot be absorbed by the Infinity Cache
+        state["keep"].append(calls[state["i"] % len(calls)]())
+        state["keep"] = state["keep"][-4:]
+        state["i"] += 1
+
+    ms, _ = time_steps(step, args.steps, args.warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"{kind}: {ms * 1e3:.1f} us/step, {nbytes / 1e6:.1f} MB -> {gbs:.0f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    result = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 5),
+        "dtype": "bf16",
+        "config": dict({"workload": f"{kind} bandwidth shape (elementwise evidence shape)",
+                        "algorithmic_bytes_per_step": nbytes}, **shape),
+        "roofline": {"bound": "hbm", "kernel": label, "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(f"{label}_{kind}")},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import elementwise as ref
+
+        torch.set_num_threads(cpu_threads())
+        if kind == "rmsnorm":
+            xc, wc = xs[0].float().cpu(), w.float().cpu()
+            secs = timed_cpu(lambda: ref.rms_norm(xc, wc, 1e-5))
+            sample = "the full x (fp32 upcast), oracle.elementwise.rms_norm"
+        elif kind == "swiglu":
+            gc, uc = gs[0][:4096].float().cpu(), us[0][:4096].float().cpu()
+            secs = timed_cpu(lambda: ref.swiglu(gc, uc)) * (gs[0].shape[0] / 4096)
+            sample = "rows 0-4095 of g, u (fp32 upcast), oracle.elementwise.swiglu, scaled x4"
+        else:
+            qc, kc = pairs[0][0].float().cpu(), pairs[0][1].float().cpu()
+            cc, sc = cos.float().cpu(), sin.float().cpu()
+            secs = timed_cpu(lambda: (ref.apply_rope(qc, cc, sc), ref.apply_rope(kc, cc, sc)))
+            sample = "the full Q and K (fp32 upcast), oracle.elementwise.apply_rope"
+        cpu_gbs = nbytes / secs / 1e9
+        log(f"cpu oracle: {secs:.3f} s -> {cpu_gbs:.2f} GB/s ({torch.get_num_threads()} threads)")
+        result["cpu_baseline"] = {"value": round(cpu_gbs, 3), "unit": "GB/s",
+                                  "cores": torch.get_num_threads(), "kind": "port",
+                                  "sample": f"{sample}: {secs:.3f} s per step"}
+    return result
+
+
 def run_copycal(args):
     """Plain device copy of a known size (256 MiB bf16 -> 256 MiB): the
     calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -430,7 +524,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="decode8b",
-                        choices=["decode8b", "decode70b", "prefill", "model8b", "copycal"])
+                        choices=["decode8b", "decode70b", "prefill", "model8b", "copycal",
+                                 "rmsnorm", "swiglu", "rope"])
     parser.add_argument("--split-tokens", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     args = parser.parse_args()
@@ -458,6 +553,8 @@ def main() -> int:
         res = run_prefill(args)
     elif args.workload == "copycal":
         res = run_copycal(args)
+    elif args.workload in ("rmsnorm", "swiglu", "rope"):
+        res = run_elementwise(args, args.workload)
     else:
         res = run_model(args)
     line = {

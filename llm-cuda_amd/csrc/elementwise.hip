@@ -230,10 +230,13 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor t1, RopeTensor t2,
   const bool second = row >= rows1;
   const RopeTensor& t = second ? t2 : t1;
   const int64_t r = second ? row - rows1 : row;
-  const int s = static_cast<int>(r % S);
-  const int64_t bh = r / S;
-  const int64_t h = bh % t.h;
-  const int64_t b = bh / t.h;
+  // Rows are ordered (b, s, h), heads fastest: neighbouring rows share one
+  // cos/sin row (served from L1 after the first), and for activations laid
+  // out as [B, S, H, D] projection views they are also adjacent in memory.
+  const int64_t h = r % t.h;
+  const int64_t bs = r / t.h;
+  const int s = static_cast<int>(bs % S);
+  const int64_t b = bs / S;
 
   const T* xp = static_cast<const T*>(t.x) + b * t.xs[0] + h * t.xs[1] + (int64_t)s * t.xs[2];
   T* op = static_cast<T*>(t.out) + b * t.os[0] + h * t.os[1] + (int64_t)s * t.os[2];
