@@ -277,13 +277,12 @@ def run_model(args):
     ids = torch.randint(0, cfg.vocab_size, (B, 1), generator=gd, device=dev)
 
     def reset():
+        cache.seq_lens_all.fill_(ctx)
         for layer in cache.layer_caches:
-            layer.seq_lens.fill_(ctx)
             layer.lengths = [ctx] * B
 
     def step():
-        for layer in cache.layer_caches:
-            layer.seq_lens.fill_(ctx)
+        cache.seq_lens_all.fill_(ctx)  # every layer's seq_lens (rows of one tensor)
         out = model(input_ids=ids, past_key_values=cache, use_cache=True)
         return torch.argmax(out["logits"][:, -1, :], dim=-1), out["logits"]
 

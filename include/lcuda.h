@@ -62,6 +62,17 @@ LC_API int lc_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, i
                    int64_t x_row_stride, int64_t y_row_stride, float eps, int dtype,
                    int w_dtype, void* stream);
 
+/* Residual add fused with RMSNorm: s = x + residual (rounded to dtype, as a
+ * torch add in that dtype), sum_out = s, y = rmsnorm(s) * w.
+ * Replaces the pair `x = x + attn_out; post_attention_layernorm(x)` of
+ * models/llama3/model.py:29-42 (one HBM pass instead of three).
+ * x, residual, y, sum_out: [rows, hidden] with row strides; sum_out may be x
+ * or residual (in place) but y must not alias any input. */
+LC_API int lc_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y,
+                       void* sum_out, int64_t rows, int64_t hidden, int64_t x_row_stride,
+                       int64_t r_row_stride, int64_t y_row_stride, int64_t s_row_stride,
+                       float eps, int dtype, int w_dtype, void* stream);
+
 /* SwiGLU forward: out = silu(gate) * up = gate * sigmoid(gate) * up (fp32 math).
  * Replaces csrc/rmsnorm_extension.cpp:25-40 (swiglu_forward),
  * csrc/swiglu_kernel.cu:7-57 and kernels/triton/swiglu.py:15-42,91-145.

@@ -13,18 +13,54 @@ namespace {
 // per lane) so it is read from HBM once; ITEMS == 0 selects a two-pass loop
 // for rows too wide to cache (re-read hits L2).
 // Follows kernels/cuda/csrc/rmsnorm_kernel.cu:26-49: y = (x * inv_rms) * w.
+// ADD: the input row is s = x + r rounded to T (the decoder layer's residual
+// add, models/llama3/model.py:29-42), written to s_out and then normalised.
 // ---------------------------------------------------------------------------
-template <typename T, typename W, int VEC, int ITEMS>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x,
-                                                      const W* __restrict__ w,
+template <typename T, typename W, int VEC, int ITEMS, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __restrict__ w,
                                                       T* __restrict__ y, int hidden,
-                                                      int64_t xs, int64_t ys, float eps) {
+                                                      int64_t xs, int64_t ys, float eps,
+                                                      const T* r, int64_t rs, T* s_out,
+                                                      int64_t ss) {
   const int64_t row = blockIdx.x;
+  // (x may alias s_out: every element is read by the thread that writes it)
   const T* xr = x + row * xs;
   T* yr = y + row * ys;
+  const T* rr = ADD ? r + row * rs : nullptr;
+  T* sr = ADD ? s_out + row * ss : nullptr;
   const int nvec = hidden / VEC;
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
+
+  // Loads vector vi of the input row (x, or round(x + r)) as fp32.
+  auto load_row = [&](int vi, float (&v)[VEC]) {
+    if constexpr (VEC * sizeof(T) == 16) {
+      Vec16<T> a = lc_load16(xr + (int64_t)vi * VEC);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = lc_to_f32(a.v[e]);
+      if constexpr (ADD) {
+        Vec16<T> b = lc_load16(rr + (int64_t)vi * VEC);
+        Vec16<T> sum;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          sum.v[e] = lc_from_f32<T>(v[e] + lc_to_f32(b.v[e]));
+          v[e] = lc_to_f32(sum.v[e]);
+        }
+        lc_store16(sr + (int64_t)vi * VEC, sum);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t c = (int64_t)vi * VEC + e;
+        v[e] = lc_to_f32(xr[c]);
+        if constexpr (ADD) {
+          const T sum = lc_from_f32<T>(v[e] + lc_to_f32(rr[c]));
+          sr[c] = sum;
+          v[e] = lc_to_f32(sum);
+        }
+      }
+    }
+  };
 
   float acc = 0.f;
   float cache[ITEMS > 0 ? ITEMS : 1][VEC];
@@ -33,25 +69,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x,
     for (int it = 0; it < ITEMS; ++it) {
       const int vi = tid + it * nthreads;
       if (vi < nvec) {
-        if constexpr (VEC * sizeof(T) == 16) {
-          Vec16<T> v = lc_load16(xr + (int64_t)vi * VEC);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) cache[it][e] = lc_to_f32(v.v[e]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) cache[it][e] = lc_to_f32(xr[(int64_t)vi * VEC + e]);
-        }
+        load_row(vi, cache[it]);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc = fmaf(cache[it][e], cache[it][e], acc);
       }
     }
   } else {
     for (int vi = tid; vi < nvec; vi += nthreads) {
+      float v[VEC];
+      load_row(vi, v);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float f = lc_to_f32(xr[(int64_t)vi * VEC + e]);
-        acc = fmaf(f, f, acc);
-      }
+      for (int e = 0; e < VEC; ++e) acc = fmaf(v[e], v[e], acc);
     }
   }
 
@@ -75,60 +103,97 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x,
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
           const float wv = lc_to_f32(w[(int64_t)vi * VEC + e]);
-          const T r = lc_from_f32<T>(cache[it][e] * inv_rms * wv);
+          const T rv = lc_from_f32<T>(cache[it][e] * inv_rms * wv);
           if constexpr (VEC * sizeof(T) == 16) {
-            out.v[e] = r;
+            out.v[e] = rv;
           } else {
-            dst[e] = r;
+            dst[e] = rv;
           }
         }
         if constexpr (VEC * sizeof(T) == 16) lc_store16(dst, out);
       }
     }
   } else {
+    // Second pass re-reads the input row (the stored sum when ADD; the same
+    // thread wrote it).
+    const T* src = ADD ? sr : xr;
     for (int vi = tid; vi < nvec; vi += nthreads) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const int64_t c = (int64_t)vi * VEC + e;
-        yr[c] = lc_from_f32<T>(lc_to_f32(xr[c]) * inv_rms * lc_to_f32(w[c]));
+        yr[c] = lc_from_f32<T>(lc_to_f32(src[c]) * inv_rms * lc_to_f32(w[c]));
       }
     }
   }
 }
 
-template <typename T, typename W, int VEC>
+template <typename T, typename W, int VEC, bool ADD>
 int launch_rmsnorm_vec(const T* x, const W* w, T* y, int64_t rows, int64_t hidden, int64_t xs,
-                       int64_t ys, float eps, hipStream_t st) {
+                       int64_t ys, float eps, const T* r, int64_t rs, T* s_out, int64_t ss,
+                       hipStream_t st) {
   const int64_t nvec = hidden / VEC;
   int threads = static_cast<int>(lc_cdiv(nvec, 64) * 64);
   if (threads > 256) threads = 256;
   if (threads < 64) threads = 64;
   const int64_t items = lc_cdiv(nvec, threads);
   dim3 grid(static_cast<unsigned>(rows));
+#define LC_RMS(ITEMS)                                                                       \
+  rmsnorm_kernel<T, W, VEC, ITEMS, ADD><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, \
+                                                                  ys, eps, r, rs, s_out, ss)
   if (items <= 1)
-    rmsnorm_kernel<T, W, VEC, 1><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+    LC_RMS(1);
   else if (items <= 2)
-    rmsnorm_kernel<T, W, VEC, 2><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+    LC_RMS(2);
   else if (items <= 4)
-    rmsnorm_kernel<T, W, VEC, 4><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+    LC_RMS(4);
   else if (items <= 8)
-    rmsnorm_kernel<T, W, VEC, 8><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
+    LC_RMS(8);
   else
-    rmsnorm_kernel<T, W, VEC, 0><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, ys, eps);
-  return lc_check_launch("lc_rmsnorm_fwd");
+    LC_RMS(0);
+#undef LC_RMS
+  return lc_check_launch(ADD ? "lc_add_rmsnorm_fwd" : "lc_rmsnorm_fwd");
 }
 
-template <typename T, typename W>
+template <typename T, typename W, bool ADD>
 int launch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
-                   int64_t xs, int64_t ys, float eps, hipStream_t st) {
+                   int64_t xs, int64_t ys, float eps, const void* r, int64_t rs, void* s_out,
+                   int64_t ss, hipStream_t st) {
   constexpr int V = 16 / sizeof(T);
-  const bool vec_ok = (hidden % V == 0) && (xs % V == 0) && (ys % V == 0) &&
-                      lc_aligned(x, 16) && lc_aligned(y, 16);
+  bool vec_ok = (hidden % V == 0) && (xs % V == 0) && (ys % V == 0) && lc_aligned(x, 16) &&
+                lc_aligned(y, 16);
+  if (ADD) vec_ok = vec_ok && rs % V == 0 && ss % V == 0 && lc_aligned(r, 16) && lc_aligned(s_out, 16);
   if (vec_ok)
-    return launch_rmsnorm_vec<T, W, V>(static_cast<const T*>(x), static_cast<const W*>(w),
-                                       static_cast<T*>(y), rows, hidden, xs, ys, eps, st);
-  return launch_rmsnorm_vec<T, W, 1>(static_cast<const T*>(x), static_cast<const W*>(w),
-                                     static_cast<T*>(y), rows, hidden, xs, ys, eps, st);
+    return launch_rmsnorm_vec<T, W, V, ADD>(
+        static_cast<const T*>(x), static_cast<const W*>(w), static_cast<T*>(y), rows, hidden, xs,
+        ys, eps, static_cast<const T*>(r), rs, static_cast<T*>(s_out), ss, st);
+  return launch_rmsnorm_vec<T, W, 1, ADD>(
+      static_cast<const T*>(x), static_cast<const W*>(w), static_cast<T*>(y), rows, hidden, xs,
+      ys, eps, static_cast<const T*>(r), rs, static_cast<T*>(s_out), ss, st);
+}
+
+template <bool ADD>
+int dispatch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
+                     int64_t xs, int64_t ys, float eps, const void* r, int64_t rs, void* s_out,
+                     int64_t ss, int dtype, int w_dtype, hipStream_t st) {
+  const bool wf = w_dtype == LC_DTYPE_F32;
+  switch (dtype) {
+    case LC_DTYPE_F32:
+      return launch_rmsnorm<float, float, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs, s_out,
+                                               ss, st);
+    case LC_DTYPE_BF16:
+      return wf ? launch_rmsnorm<bf16_t, float, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
+                                                     s_out, ss, st)
+                : launch_rmsnorm<bf16_t, bf16_t, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
+                                                      s_out, ss, st);
+    case LC_DTYPE_F16:
+      return wf ? launch_rmsnorm<f16_t, float, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
+                                                    s_out, ss, st)
+                : launch_rmsnorm<f16_t, f16_t, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
+                                                    s_out, ss, st);
+    default:
+      return lc_fail(LC_EINVAL, "%s: unknown dtype %d",
+                     ADD ? "lc_add_rmsnorm_fwd" : "lc_rmsnorm_fwd", dtype);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -334,26 +399,26 @@ int lc_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t 
   LC_REQUIRE(w_dtype == dtype || w_dtype == LC_DTYPE_F32,
              "lc_rmsnorm_fwd: weight dtype must equal x dtype or be fp32");
   if (rows == 0) return LC_OK;
-  hipStream_t st = lc_stream(stream);
-  switch (dtype) {
-    case LC_DTYPE_F32:
-      return launch_rmsnorm<float, float>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps,
-                                          st);
-    case LC_DTYPE_BF16:
-      return w_dtype == LC_DTYPE_F32
-                 ? launch_rmsnorm<bf16_t, float>(x, w, y, rows, hidden, x_row_stride,
-                                                 y_row_stride, eps, st)
-                 : launch_rmsnorm<bf16_t, bf16_t>(x, w, y, rows, hidden, x_row_stride,
-                                                  y_row_stride, eps, st);
-    case LC_DTYPE_F16:
-      return w_dtype == LC_DTYPE_F32
-                 ? launch_rmsnorm<f16_t, float>(x, w, y, rows, hidden, x_row_stride,
-                                                y_row_stride, eps, st)
-                 : launch_rmsnorm<f16_t, f16_t>(x, w, y, rows, hidden, x_row_stride,
-                                                y_row_stride, eps, st);
-    default:
-      return lc_fail(LC_EINVAL, "lc_rmsnorm_fwd: unknown dtype %d", dtype);
-  }
+  return dispatch_rmsnorm<false>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, nullptr,
+                                 0, nullptr, 0, dtype, w_dtype, lc_stream(stream));
+}
+
+int lc_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y,
+                       void* sum_out, int64_t rows, int64_t hidden, int64_t x_row_stride,
+                       int64_t r_row_stride, int64_t y_row_stride, int64_t s_row_stride,
+                       float eps, int dtype, int w_dtype, void* stream) {
+  LC_REQUIRE(rows >= 0 && hidden > 0, "lc_add_rmsnorm_fwd: bad shape rows=%lld hidden=%lld",
+             (long long)rows, (long long)hidden);
+  LC_REQUIRE(hidden < (1LL << 31) && rows < (1LL << 31), "lc_add_rmsnorm_fwd: shape too large");
+  LC_REQUIRE(x && residual && w && y && sum_out, "lc_add_rmsnorm_fwd: null pointer");
+  LC_REQUIRE(w_dtype == dtype || w_dtype == LC_DTYPE_F32,
+             "lc_add_rmsnorm_fwd: weight dtype must equal x dtype or be fp32");
+  LC_REQUIRE(y != sum_out && y != x && y != residual,
+             "lc_add_rmsnorm_fwd: y must not alias x, residual or sum_out");
+  if (rows == 0) return LC_OK;
+  return dispatch_rmsnorm<true>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, residual,
+                                r_row_stride, sum_out, s_row_stride, dtype, w_dtype,
+                                lc_stream(stream));
 }
 
 int lc_swiglu_fwd(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,

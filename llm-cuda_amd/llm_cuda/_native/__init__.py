@@ -39,6 +39,11 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, ctypes.c_int,
          ctypes.c_int, _c_p],
     ),
+    "lc_add_rmsnorm_fwd": (
+        ctypes.c_int,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, ctypes.c_int, ctypes.c_int, _c_p],
+    ),
     "lc_swiglu_fwd": (
         ctypes.c_int,
         [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_p],

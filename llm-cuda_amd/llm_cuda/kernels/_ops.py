@@ -69,6 +69,42 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return y.view(x.shape)
 
 
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+                 inplace: bool = False):
+    """s = x + residual (rounded to x's dtype), y = rms_norm(s) * weight; returns (y, s).
+
+    One pass over the rows instead of an add and a norm (reference pair:
+    models/llama3/model.py:29-42). With inplace=True, s is written into x.
+    """
+    dev = nat.require_device(x, residual, weight)
+    if x.shape != residual.shape or x.dtype != residual.dtype:
+        raise ValueError("x and residual must have the same shape and dtype")
+    if weight.dim() != 1 or weight.shape[0] != x.shape[-1]:
+        raise ValueError(f"weight shape {tuple(weight.shape)} does not match hidden {x.shape[-1]}")
+    hidden = x.shape[-1]
+    x2 = x.reshape(-1, hidden)
+    r2 = residual.reshape(-1, hidden)
+    if inplace and (x2.data_ptr() != x.data_ptr() or x2.stride(-1) != 1):
+        raise ValueError("inplace add_rms_norm needs x with unit stride over hidden")
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if r2.stride(-1) != 1:
+        r2 = r2.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    if w.dtype != x.dtype and w.dtype != torch.float32:
+        w = w.to(x.dtype)
+    y = torch.empty((x2.shape[0], hidden), dtype=x.dtype, device=dev)
+    s2 = x2 if inplace else torch.empty((x2.shape[0], hidden), dtype=x.dtype, device=dev)
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_add_rmsnorm_fwd(
+            x2.data_ptr(), r2.data_ptr(), w.data_ptr(), y.data_ptr(), s2.data_ptr(), x2.shape[0],
+            hidden, x2.stride(0), r2.stride(0), y.stride(0), s2.stride(0), float(eps),
+            nat.lc_dtype(x), nat.lc_dtype(w), _stream(dev))
+    nat.check(rc, "lc_add_rmsnorm_fwd")
+    return y.view(x.shape), (x if inplace else s2.view(x.shape))
+
+
 # ---------------------------------------------------------------------------
 # SwiGLU  (reference: kernels/triton/swiglu.py:91-145,199-200)
 # ---------------------------------------------------------------------------

@@ -3,8 +3,12 @@
 Same module, parameters and call signature as the reference. The forward pass
 differs only in how the attention itself is computed, all on HIP kernels:
 
+  * Inference projections: q, k and v come out of one GEMM against the
+    concatenated weight (the parameters alias its row blocks).
   * RoPE: Q and K rotated in one launch, reading the transposed projection
-    views directly.
+    views directly. The cos/sin tables are built once for a range of
+    positions and sliced per call (every row depends only on its position,
+    so the slices equal the per-call tables of rotary.py:29-71).
   * Paged cache, one query token (decode): new K/V are scattered into the page
     pools and the query attends to the pools in place through the block table
     (split-K flash-decode). The reference instead copied the whole cache into a
@@ -18,6 +22,7 @@ from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
 from llm_cuda.kernels.triton.decode_attention import (
@@ -26,6 +31,7 @@ from llm_cuda.kernels.triton.decode_attention import (
 )
 
 from .config import Llama3Config
+from .fused import FusedLinearWeights
 from .kv_cache import PagedKVLayerCache
 from .rotary import apply_rotary, build_inv_freq, build_rope_cache
 
@@ -53,6 +59,26 @@ class Llama3Attention(nn.Module):
         inv_freq = build_inv_freq(
             head_dim=config.head_dim, base=config.rope_theta, device=torch.device("cpu"))
         self.register_buffer("inv_freq", inv_freq, persistent=False)
+        self._qkv = FusedLinearWeights(self.q_proj, self.k_proj, self.v_proj)
+        self._rope_cache: tuple | None = None
+
+    def _rope_tables(self, past_len: int, seq_len: int, device: torch.device,
+                     dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        """cos, sin [seq_len, D] for positions past_len .. +seq_len-1, sliced from a
+        table over positions 0 .. cap-1 (rebuilt when inv_freq, the device or the
+        dtype change, and doubled when a position falls outside it)."""
+        need = past_len + seq_len
+        inv = self.inv_freq
+        key = (inv.data_ptr(), inv._version, inv.dtype, device, dtype)
+        cache = self._rope_cache
+        if cache is None or cache[0] != key or cache[1] < need:
+            cap = max(need, 256, 2 * cache[1] if cache is not None and cache[0] == key else 0)
+            cap = 1 << (cap - 1).bit_length()
+            cos, sin = build_rope_cache(
+                seq_len=cap, head_dim=self.head_dim, base=self.config.rope_theta,
+                device=device, dtype=dtype, position_offset=0, inv_freq=inv)
+            cache = self._rope_cache = (key, cap, cos, sin)
+        return cache[2][past_len:need], cache[3][past_len:need]
 
     def _shape(self, x: torch.Tensor, heads: int) -> torch.Tensor:
         bsz, seq_len, _ = x.shape
@@ -70,9 +96,16 @@ class Llama3Attention(nn.Module):
                 "additive attention masks are not supported by the HIP attention kernels")
         bsz, seq_len, _ = x.shape
 
-        q = self._shape(self.q_proj(x), self.num_heads)
-        k = self._shape(self.k_proj(x), self.num_kv_heads)
-        v = self._shape(self.v_proj(x), self.num_kv_heads)
+        if FusedLinearWeights.usable(self.q_proj, self.k_proj, self.v_proj):
+            nq, nk, _ = self._qkv.sizes()
+            qkv = F.linear(x, self._qkv.weight())
+            q = self._shape(qkv[..., :nq], self.num_heads)
+            k = self._shape(qkv[..., nq:nq + nk], self.num_kv_heads)
+            v = self._shape(qkv[..., nq + nk:], self.num_kv_heads)
+        else:
+            q = self._shape(self.q_proj(x), self.num_heads)
+            k = self._shape(self.k_proj(x), self.num_kv_heads)
+            v = self._shape(self.v_proj(x), self.num_kv_heads)
 
         paged = isinstance(past_key_value, PagedKVLayerCache)
         if paged:
@@ -82,15 +115,7 @@ class Llama3Attention(nn.Module):
         else:
             past_len = 0
 
-        cos, sin = build_rope_cache(
-            seq_len=seq_len,
-            head_dim=self.head_dim,
-            base=self.config.rope_theta,
-            device=x.device,
-            dtype=x.dtype,
-            position_offset=past_len,
-            inv_freq=self.inv_freq,
-        )
+        cos, sin = self._rope_tables(past_len, seq_len, x.device, x.dtype)
         q, k = apply_rotary(q, k, cos, sin)
 
         if paged:

@@ -36,6 +36,7 @@ class PagedKVLayerCache:
         batch_size: int = 1,
         block_table: torch.Tensor | None = None,
         num_pages: int | None = None,
+        seq_lens: torch.Tensor | None = None,
     ):
         if page_size <= 0:
             raise ValueError("page_size must be > 0")
@@ -71,7 +72,14 @@ class PagedKVLayerCache:
         self.key_pages = torch.empty(
             pool, num_kv_heads, page_size, head_dim, device=device, dtype=dtype)
         self.value_pages = torch.empty_like(self.key_pages)
-        self.seq_lens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        if seq_lens is None:
+            seq_lens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        elif (seq_lens.dtype != torch.int32 or seq_lens.shape != (batch_size,)
+              or seq_lens.device != device):
+            raise ValueError(f"seq_lens must be int32 [{batch_size}] on {device}")
+        else:
+            seq_lens.zero_()
+        self.seq_lens = seq_lens
         self.lengths = [0] * batch_size
 
     @property
@@ -115,10 +123,14 @@ class PagedKVLayerCache:
 
 
 class PagedKVCache:
-    def __init__(self, layer_caches: list[PagedKVLayerCache]):
+    def __init__(self, layer_caches: list[PagedKVLayerCache],
+                 seq_lens_all: torch.Tensor | None = None):
         if not layer_caches:
             raise ValueError("layer_caches must not be empty")
         self.layer_caches = layer_caches
+        # [num_layers, batch] int32 whose rows are the layers' seq_lens when the
+        # cache was made by create(): one fill resets every layer's lengths.
+        self.seq_lens_all = seq_lens_all
 
     @classmethod
     def create(
@@ -134,6 +146,8 @@ class PagedKVCache:
         block_table: torch.Tensor | None = None,
         num_pages: int | None = None,
     ) -> "PagedKVCache":
+        device = torch.device(device)
+        lens = torch.zeros(num_layers, batch_size, dtype=torch.int32, device=device)
         return cls(
             [
                 PagedKVLayerCache(
@@ -146,9 +160,11 @@ class PagedKVCache:
                     batch_size=batch_size,
                     block_table=block_table,
                     num_pages=num_pages,
+                    seq_lens=lens[i],
                 )
-                for _ in range(num_layers)
-            ]
+                for i in range(num_layers)
+            ],
+            seq_lens_all=lens,
         )
 
     def get_layer(self, layer_idx: int) -> PagedKVLayerCache:

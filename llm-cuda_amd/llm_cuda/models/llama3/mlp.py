@@ -1,14 +1,17 @@
 """Llama-3 MLP (reference: models/llama3/mlp.py:1-43): down(silu(gate(x)) * up(x)).
 
 The projections are torch matmuls (hipBLASLt); the SwiGLU between them is the
-HIP kernel.
+HIP kernel. For inference, gate and up come out of one GEMM against the
+concatenated weight and SwiGLU reads the two halves of its output in place.
 """
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from llm_cuda.kernels.triton.swiglu import triton_swiglu
 
 from .config import Llama3Config
+from .fused import FusedLinearWeights
 
 
 class Llama3MLP(nn.Module):
@@ -19,6 +22,11 @@ class Llama3MLP(nn.Module):
         self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+        self._gate_up = FusedLinearWeights(self.gate_proj, self.up_proj)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if FusedLinearWeights.usable(self.gate_proj, self.up_proj):
+            n = self.gate_proj.weight.shape[0]
+            gu = F.linear(x, self._gate_up.weight())
+            return self.down_proj(triton_swiglu(gu[..., :n], gu[..., n:]))
         return self.down_proj(triton_swiglu(self.gate_proj(x), self.up_proj(x)))

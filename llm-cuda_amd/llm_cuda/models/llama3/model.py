@@ -14,6 +14,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from llm_cuda.kernels._ops import add_rms_norm
+
 from .attention import Llama3Attention
 from .config import Llama3Config
 from .kv_cache import PagedKVCache, PagedKVLayerCache
@@ -42,8 +44,11 @@ class Llama3DecoderLayer(nn.Module):
             past_key_value=past_key_value,
             use_cache=use_cache,
         )
-        x = x + attn_out
-        x = x + self.mlp(self.post_attention_layernorm(x))
+        # x = x + attn_out and its post-attention norm in one HIP pass
+        # (the sum is rounded to x's dtype exactly as the separate add).
+        norm = self.post_attention_layernorm
+        h, x = add_rms_norm(x, attn_out, norm.weight, norm.eps)
+        x = x + self.mlp(h)
         return x, present
 
 

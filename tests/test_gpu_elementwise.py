@@ -50,6 +50,44 @@ def test_rmsnorm_constant_row_closed_form(cuda):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 4, 16), (32, 1, 4096), (2, 20480), (3, 1001)])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_add_rmsnorm(cuda, dtype, shape, inplace):
+    """Fused residual add + RMSNorm: the sum equals torch's add in the storage
+    dtype bit for bit, and y equals the oracle's rms_norm of that sum. Widths
+    cover the register-cached path, the two-pass path (20480 > 256 lanes x 8
+    vectors x 8) and the element-wise path (1001)."""
+    from llm_cuda.kernels._ops import add_rms_norm
+
+    torch.manual_seed(42)
+    x = torch.randn(*shape, device=cuda).to(dtype)
+    r = torch.randn(*shape, device=cuda).to(dtype)
+    w = (1 + 0.1 * torch.randn(shape[-1], device=cuda)).to(dtype)
+    ref_sum = x + r
+    x_in = x.clone()
+    y, s = add_rms_norm(x_in, r, w, 1e-5, inplace=inplace)
+    assert torch.equal(s, ref_sum)
+    if inplace:
+        assert s.data_ptr() == x_in.data_ptr() and torch.equal(x_in, ref_sum)
+    else:
+        assert torch.equal(x_in, x)
+    assert_close(y, rms_norm(ref_sum.cpu(), w.cpu(), 1e-5), ATOL[dtype], "add_rmsnorm",
+                 rtol=RTOL[dtype])
+
+
+def test_add_rmsnorm_strided_and_fp32_weight(cuda):
+    from llm_cuda.kernels._ops import add_rms_norm
+
+    torch.manual_seed(43)
+    base = torch.randn(5, 600, device=cuda).to(torch.bfloat16)
+    x, r = base[:, :256], base[:, 300:556]  # row stride 600
+    w = torch.randn(256, device=cuda)
+    y, s = add_rms_norm(x, r, w, 1e-6)
+    assert torch.equal(s, x + r)
+    assert_close(y, rms_norm((x + r).cpu(), w.cpu(), 1e-6), ATOL[torch.bfloat16], "strided")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("shape", [(2, 4, 16), (1, 8, 64), (32, 1, 14336), (3, 1001)])
 def test_swiglu(cuda, dtype, shape):
     from llm_cuda.kernels.triton.swiglu import triton_swiglu

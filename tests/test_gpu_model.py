@@ -152,3 +152,49 @@ def test_bf16_8b_layer_shape_paged_vs_full(cuda):
     got = torch.cat(steps, 1).float()
     scale = full[:, 66:].abs().max().item()
     assert (got - full[:, 66:]).abs().max().item() <= 3e-2 * max(1.0, scale)
+
+
+def test_fused_projections_match_separate(cuda):
+    """Inference runs q/k/v and gate/up as one GEMM each against the concatenated
+    weights; with autograd recording, the separate Linear calls run. Both give
+    the same logits (fp32, GEMM reassociation only), and the parameters alias
+    the fused buffers afterwards."""
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(7)
+    cfg = _small_config()
+    model = Llama3ForCausalLM(cfg).to(cuda).eval()
+    ids = torch.randint(0, cfg.vocab_size, (2, 9), device=cuda)
+    separate = model(input_ids=ids)["logits"].detach()
+    with torch.no_grad():
+        fused = model(input_ids=ids)["logits"]
+    assert (fused - separate).abs().max().item() < 1e-4
+    attn, mlp = model.model.layers[0].self_attn, model.model.layers[0].mlp
+    buf = attn._qkv.buf
+    assert buf is not None and attn.q_proj.weight.data_ptr() == buf.data_ptr()
+    assert mlp.up_proj.weight.data_ptr() == mlp._gate_up.buf.data_ptr() + \
+        mlp.gate_proj.weight.numel() * mlp.gate_proj.weight.element_size()
+    # a state-dict load writes through the aliases into the fused buffers
+    sd = {k: torch.randn_like(v) for k, v in model.state_dict().items()}
+    model.load_state_dict(sd)
+    with torch.no_grad():
+        after = model(input_ids=ids)["logits"]
+    ref = Llama3ForCausalLM(cfg).to(cuda).eval()
+    ref.load_state_dict(sd)
+    assert (after - ref(input_ids=ids)["logits"].detach()).abs().max().item() < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rope_table_cache_is_bit_exact(cuda, dtype):
+    """Slices of the cached all-positions table equal the per-call tables of
+    rotary.build_rope_cache bit for bit, across a cache growth."""
+    from llm_cuda.models.llama3.attention import Llama3Attention
+    from llm_cuda.models.llama3.rotary import build_rope_cache
+
+    cfg = _small_config(max_position_embeddings=4096)
+    attn = Llama3Attention(cfg).to(device=cuda, dtype=dtype)
+    for past, n in [(0, 7), (5, 1), (255, 3), (300, 1), (1000, 40)]:
+        cos, sin = attn._rope_tables(past, n, torch.device(cuda), dtype)
+        rc, rs = build_rope_cache(n, cfg.head_dim, cfg.rope_theta, torch.device(cuda), dtype,
+                                  position_offset=past, inv_freq=attn.inv_freq)
+        assert torch.equal(cos, rc) and torch.equal(sin, rs)
