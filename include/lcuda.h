@@ -160,6 +160,31 @@ LC_API int lc_paged_kv_append(const void* k_new, const void* v_new, const int64_
                        int64_t num_pages, const int32_t* start_pos, int64_t B, int64_t Hkv,
                        int64_t S, int64_t D, int64_t page_size, int dtype, void* stream);
 
+/* Decode-time RoPE + cache append in one launch (one workgroup per sequence).
+ * With p = seq_lens[b] + s for s < S:
+ *   q_out[b, h, s, :] = rope(q[b, h, s, :], p)                       h < Hq
+ *   key_pages[bt[b, p/P], h, p%P, :] = rope(k[b, h, s, :], p)        h < Hkv
+ *   value_pages[bt[b, p/P], h, p%P, :] = v[b, h, s, :]
+ * then seq_lens[b] += S (int32 [B], device, read and advanced in place).
+ * rope(x, p) = x * cos[p] + rotate_half(x) * sin[p] in fp32, rounded once,
+ * with full-width tables cos/sin [table_rows, D] (row strides cos_stride /
+ * sin_stride) that must cover the block-table capacity.
+ * Replaces the decode-step sequence RoPE (kernels/triton/rope.py:156-222 via
+ * models/llama3/rotary.py:81-109) then PagedKVLayerCache.append
+ * (models/llama3/kv_cache.py:38-63) of models/llama3/attention.py:100-124.
+ * q, k, v, q_out: [B, H, S, D] with strides (any, head_dim stride 1). Tokens
+ * whose page entry is invalid are dropped from the cache, as in
+ * lc_paged_kv_append. */
+LC_API int lc_rope_kv_append(const void* q, const int64_t* q_strides, const void* k,
+                      const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                      void* q_out, const int64_t* q_out_strides, const void* cos,
+                      const void* sin, int64_t cos_stride, int64_t sin_stride,
+                      int64_t table_rows, void* key_pages, void* value_pages, int64_t kv_s_page,
+                      int64_t kv_s_head, int64_t kv_s_tok, const int32_t* block_table,
+                      int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
+                      int32_t* seq_lens, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                      int64_t page_size, int dtype, void* stream);
+
 /* Gather the first L tokens of every sequence into contiguous
  * k_out, v_out [B, Hkv, L, D] (bit-exact copy through the block table).
  * Replaces models/llama3/kv_cache.py:65-83 (PagedKVLayerCache.get_kv).

@@ -143,6 +143,136 @@ int launch_gather(const KvPool& pool, void* ko, void* vo, int64_t B, int64_t Hkv
   return lc_check_launch("lc_paged_kv_gather");
 }
 
+// Decode-time fusion of RoPE with the cache append (one workgroup per
+// sequence b, positions p = seq_lens[b] + s):
+//   q_out[b, h, s]                      = rope(q[b, h, s], p)
+//   key_pages[page(b, p), h, p % P]     = rope(k[b, h, s], p)
+//   value_pages[page(b, p), h, p % P]   = v[b, h, s]
+// then seq_lens[b] += S. The rotation is the RoPE kernel's (full-width
+// tables, fp32, one rounding): lo = x1 c1 - x2 s1, hi = x2 c2 + x1 s2 over the
+// two halves of the row; cos/sin rows are indexed by p, so a captured graph
+// stays valid at any position.
+struct RopeAppendArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* qo;
+  int64_t qs[3], ks[3], vs[3], qos[3];  // (b, h, s) element strides; d stride 1
+  const void* cos;
+  const void* sin;
+  int64_t cs, ss;  // table row strides
+  int table_rows;
+  int32_t* seq_lens;
+  int Hq, Hkv, S, D;
+};
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void rope_kv_append_kernel(KvPool pool, RopeAppendArgs a) {
+  const int b = blockIdx.x;
+  const int start = a.seq_lens[b];  // every thread reads it before the update below
+  const int half = a.D / 2;
+  const int hc = half / VEC;  // rotated chunk pairs per row
+  const int vc = a.D / VEC;   // copied chunks per V row
+  const int nq = a.S * a.Hq * hc;
+  const int nk = a.S * a.Hkv * hc;
+  const int nv = a.S * a.Hkv * vc;
+  const T* cos = static_cast<const T*>(a.cos);
+  const T* sin = static_cast<const T*>(a.sin);
+  for (int i = threadIdx.x; i < nq + nk + nv; i += blockDim.x) {
+    if (i < nq + nk) {
+      const bool isk = i >= nq;
+      const int j = isk ? i - nq : i;
+      const int heads = isk ? a.Hkv : a.Hq;
+      const int c = j % hc;
+      const int hs = j / hc;
+      const int h = hs % heads;
+      const int s = hs / heads;
+      const int pos = start + s;
+      const int prow = pos < 0 ? 0 : (pos >= a.table_rows ? a.table_rows - 1 : pos);
+      const int d0 = c * VEC;
+      const T* src = isk ? static_cast<const T*>(a.k) + b * a.ks[0] + h * a.ks[1] + s * a.ks[2]
+                         : static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1] + s * a.qs[2];
+      const T* cp = cos + (int64_t)prow * a.cs;
+      const T* sp = sin + (int64_t)prow * a.ss;
+      T* dst;
+      if (isk) {
+        const int64_t off = pool_offset(pool, b, h, pos);
+        if (off < 0) continue;
+        dst = static_cast<T*>(pool.kp) + off;
+      } else {
+        dst = static_cast<T*>(a.qo) + b * a.qos[0] + h * a.qos[1] + s * a.qos[2];
+      }
+      float x1[VEC], x2[VEC], c1[VEC], c2[VEC], s1[VEC], s2[VEC];
+      if constexpr (VEC * sizeof(T) == 16) {
+        const Vec16<T> va = lc_load16(src + d0), vb = lc_load16(src + d0 + half);
+        const Vec16<T> ca = lc_load16(cp + d0), cb = lc_load16(cp + d0 + half);
+        const Vec16<T> sa = lc_load16(sp + d0), sb = lc_load16(sp + d0 + half);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          x1[e] = lc_to_f32(va.v[e]);
+          x2[e] = lc_to_f32(vb.v[e]);
+          c1[e] = lc_to_f32(ca.v[e]);
+          c2[e] = lc_to_f32(cb.v[e]);
+          s1[e] = lc_to_f32(sa.v[e]);
+          s2[e] = lc_to_f32(sb.v[e]);
+        }
+        Vec16<T> o1, o2;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          o1.v[e] = lc_from_f32<T>(x1[e] * c1[e] - x2[e] * s1[e]);
+          o2.v[e] = lc_from_f32<T>(x2[e] * c2[e] + x1[e] * s2[e]);
+        }
+        lc_store16(dst + d0, o1);
+        lc_store16(dst + d0 + half, o2);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float u1 = lc_to_f32(src[d0 + e]), u2 = lc_to_f32(src[d0 + e + half]);
+          dst[d0 + e] = lc_from_f32<T>(u1 * lc_to_f32(cp[d0 + e]) - u2 * lc_to_f32(sp[d0 + e]));
+          dst[d0 + e + half] =
+              lc_from_f32<T>(u2 * lc_to_f32(cp[d0 + e + half]) + u1 * lc_to_f32(sp[d0 + e + half]));
+        }
+      }
+    } else {
+      const int j = i - nq - nk;
+      const int c = j % vc;
+      const int hs = j / vc;
+      const int h = hs % a.Hkv;
+      const int s = hs / a.Hkv;
+      const int64_t off = pool_offset(pool, b, h, start + s);
+      if (off < 0) continue;
+      const T* src = static_cast<const T*>(a.v) + b * a.vs[0] + h * a.vs[1] + s * a.vs[2] + c * VEC;
+      T* dst = static_cast<T*>(pool.vp) + off + c * VEC;
+      if constexpr (VEC * sizeof(T) == 16) {
+        lc_store16(dst, lc_load16(src));
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dst[e] = src[e];
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) a.seq_lens[b] = start + a.S;
+}
+
+template <typename T>
+int launch_rope_append(const KvPool& pool, const RopeAppendArgs& a, int64_t B, hipStream_t st) {
+  constexpr int V = 16 / sizeof(T);
+  bool vec_ok = (a.D / 2) % V == 0 && lc_aligned(a.q, 16) && lc_aligned(a.k, 16) &&
+                lc_aligned(a.v, 16) && lc_aligned(a.qo, 16) && lc_aligned(a.cos, 16) &&
+                lc_aligned(a.sin, 16) && lc_aligned(pool.kp, 16) && lc_aligned(pool.vp, 16) &&
+                a.cs % V == 0 && a.ss % V == 0 && pool.s_page % V == 0 && pool.s_head % V == 0 &&
+                pool.s_tok % V == 0;
+  for (int i = 0; i < 3; ++i)
+    vec_ok = vec_ok && a.qs[i] % V == 0 && a.ks[i] % V == 0 && a.vs[i] % V == 0 &&
+             a.qos[i] % V == 0;
+  if (vec_ok)
+    rope_kv_append_kernel<T, V><<<(unsigned)B, 256, 0, st>>>(pool, a);
+  else
+    rope_kv_append_kernel<T, 1><<<(unsigned)B, 256, 0, st>>>(pool, a);
+  return lc_check_launch("lc_rope_kv_append");
+}
+
 int check_pool(const char* fn, int64_t s_page, int64_t s_head, int64_t s_tok,
                int64_t max_pages_per_seq, int64_t num_pages, int64_t bt_stride,
                int64_t page_size, int64_t Hkv, int64_t D) {
@@ -219,6 +349,67 @@ int lc_paged_kv_gather(const void* key_pages, const void* value_pages, int64_t k
       return launch_gather<f16_t>(pool, k_out, v_out, B, Hkv, L, D, st);
     default:
       return lc_fail(LC_EINVAL, "lc_paged_kv_gather: unknown dtype %d", dtype);
+  }
+}
+
+int lc_rope_kv_append(const void* q, const int64_t* q_strides, const void* k,
+                      const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                      void* q_out, const int64_t* q_out_strides, const void* cos,
+                      const void* sin, int64_t cos_stride, int64_t sin_stride,
+                      int64_t table_rows, void* key_pages, void* value_pages, int64_t kv_s_page,
+                      int64_t kv_s_head, int64_t kv_s_tok, const int32_t* block_table,
+                      int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
+                      int32_t* seq_lens, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                      int64_t page_size, int dtype, void* stream) {
+  LC_REQUIRE(q && q_strides && k && k_strides && v && v_strides && q_out && q_out_strides &&
+                 cos && sin && key_pages && value_pages && block_table && seq_lens,
+             "lc_rope_kv_append: null pointer");
+  LC_REQUIRE(B >= 0 && B < (1LL << 31) && Hq > 0 && S >= 0 && D > 0 && D % 2 == 0,
+             "lc_rope_kv_append: bad shape");
+  LC_REQUIRE(S * (Hq + 2 * Hkv) * D < (1LL << 30), "lc_rope_kv_append: too many new tokens");
+  LC_REQUIRE(q_strides[3] == 1 && k_strides[3] == 1 && v_strides[3] == 1 && q_out_strides[3] == 1,
+             "lc_rope_kv_append: head_dim stride must be 1");
+  int rc = check_pool("lc_rope_kv_append", kv_s_page, kv_s_head, kv_s_tok, max_pages_per_seq,
+                      num_pages, bt_stride, page_size, Hkv, D);
+  if (rc != LC_OK) return rc;
+  LC_REQUIRE(table_rows >= max_pages_per_seq * page_size && table_rows < (1LL << 31),
+             "lc_rope_kv_append: the cos/sin tables (%lld rows) must cover the block-table "
+             "capacity (%lld positions)",
+             (long long)table_rows, (long long)(max_pages_per_seq * page_size));
+  if (B == 0 || S == 0) return LC_OK;
+  KvPool pool{key_pages, value_pages, kv_s_page, kv_s_head, kv_s_tok, block_table, bt_stride,
+              (int)max_pages_per_seq, (int)num_pages, (int)page_size};
+  RopeAppendArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.qo = q_out;
+  for (int i = 0; i < 3; ++i) {
+    a.qs[i] = q_strides[i];
+    a.ks[i] = k_strides[i];
+    a.vs[i] = v_strides[i];
+    a.qos[i] = q_out_strides[i];
+  }
+  a.cos = cos;
+  a.sin = sin;
+  a.cs = cos_stride;
+  a.ss = sin_stride;
+  a.table_rows = (int)table_rows;
+  a.seq_lens = seq_lens;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.S = (int)S;
+  a.D = (int)D;
+  hipStream_t st = lc_stream(stream);
+  switch (dtype) {
+    case LC_DTYPE_F32:
+      return launch_rope_append<float>(pool, a, B, st);
+    case LC_DTYPE_BF16:
+      return launch_rope_append<bf16_t>(pool, a, B, st);
+    case LC_DTYPE_F16:
+      return launch_rope_append<f16_t>(pool, a, B, st);
+    default:
+      return lc_fail(LC_EINVAL, "lc_rope_kv_append: unknown dtype %d", dtype);
   }
 }
 

@@ -353,6 +353,49 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, key_pages: torch.Tensor,
     nat.check(rc, "lc_paged_kv_append")
 
 
+def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                   sin: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
+                   block_table: torch.Tensor, seq_lens: torch.Tensor) -> torch.Tensor:
+    """Decode-time RoPE + cache append in one launch.
+
+    Rotates q and k at positions seq_lens[b] + s (cos/sin: full tables indexed
+    by position, covering the block-table capacity), writes the rotated k and
+    v into the page pools, advances seq_lens by S in place and returns the
+    rotated q as a new contiguous [B, Hq, S, D] tensor.
+    """
+    _pool_checks(key_pages, value_pages, block_table)
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
+        raise ValueError("q must be [B, Hq, S, D] and k, v [B, Hkv, S, D]")
+    B, Hq, S, D = q.shape
+    N, Hkv, P, Dp = key_pages.shape
+    if k.shape != (B, Hkv, S, D) or Dp != D or block_table.shape[0] != B:
+        raise ValueError("q/k/v do not match the cache layout")
+    if seq_lens.dtype != torch.int32 or seq_lens.shape != (B,):
+        raise TypeError("seq_lens must be int32 [batch]")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D:
+        raise ValueError("cos/sin must be [positions, head_dim]")
+    if not (q.dtype == k.dtype == v.dtype == cos.dtype == sin.dtype == key_pages.dtype):
+        raise TypeError("q, k, v, cos, sin and the pools must share a dtype")
+    dev = nat.require_device(q, k, v, cos, sin, key_pages, value_pages, block_table, seq_lens)
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    cos = cos if cos.stride(-1) == 1 else cos.contiguous()
+    sin = sin if sin.stride(-1) == 1 else sin.contiguous()
+    q_out = torch.empty((B, Hq, S, D), dtype=q.dtype, device=dev)
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_rope_kv_append(
+            q.data_ptr(), _i64arr(q.stride()), k.data_ptr(), _i64arr(k.stride()), v.data_ptr(),
+            _i64arr(v.stride()), q_out.data_ptr(), _i64arr(q_out.stride()), cos.data_ptr(),
+            sin.data_ptr(), cos.stride(0), sin.stride(0), cos.shape[0], key_pages.data_ptr(),
+            value_pages.data_ptr(), key_pages.stride(0), key_pages.stride(1), key_pages.stride(2),
+            block_table.data_ptr(), block_table.stride(0), block_table.shape[1], N,
+            seq_lens.data_ptr(), B, Hq, Hkv, S, D, P, nat.lc_dtype(q), _stream(dev))
+    nat.check(rc, "lc_rope_kv_append")
+    return q_out
+
+
 def kv_gather(key_pages: torch.Tensor, value_pages: torch.Tensor, block_table: torch.Tensor,
               length: int):
     """Contiguous [B, Hkv, length, D] copies of the first `length` tokens."""

@@ -115,6 +115,19 @@ class Llama3Attention(nn.Module):
         else:
             past_len = 0
 
+        if paged and use_cache and seq_len == 1:
+            # Decode step: RoPE and the cache append in one launch, positions
+            # taken from the cache's device-side lengths.
+            cache = past_key_value
+            rows = cache.max_pages * cache.page_size
+            self._rope_tables(0, rows, x.device, x.dtype)
+            cos_t, sin_t = self._rope_cache[2], self._rope_cache[3]
+            q = cache.append_rotated(q, k, v, cos_t, sin_t)
+            out = paged_decode_attention(
+                q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens)
+            out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
+            return self.o_proj(out), cache
+
         cos, sin = self._rope_tables(past_len, seq_len, x.device, x.dtype)
         q, k = apply_rotary(q, k, cos, sin)
 

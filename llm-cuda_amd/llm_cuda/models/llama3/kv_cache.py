@@ -109,6 +109,27 @@ class PagedKVLayerCache:
         self.seq_lens.add_(seq)
         self.lengths = [n + seq for n in self.lengths]
 
+    def append_rotated(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """Decode-time fusion of RoPE and `append`: rotates q and k at the
+        positions seq_lens[b] + s, appends the rotated k and v, and returns the
+        rotated q. cos/sin are full tables indexed by position that cover
+        max_pages * page_size positions."""
+        if k.shape != v.shape or k.dim() != 4 or q.dim() != 4:
+            raise ValueError("Expected q, k, v of shape [batch, heads, seq, head_dim]")
+        if k.shape[0] != self.batch_size or q.shape[0] != self.batch_size:
+            raise ValueError(
+                f"batch {k.shape[0]} does not match the cache batch size {self.batch_size}")
+        if k.shape[1] != self.num_kv_heads or k.shape[3] != self.head_dim:
+            raise ValueError("k/v shapes do not match cache layout")
+        seq = k.shape[2]
+        if max(self.lengths) + seq > self.max_seq_len:
+            raise ValueError("Appending would exceed max_seq_len")
+        q_rot = _ops.rope_kv_append(q, k, v, cos, sin, self.key_pages, self.value_pages,
+                                    self.block_table, self.seq_lens)
+        self.lengths = [n + seq for n in self.lengths]
+        return q_rot
+
     def get_kv(self) -> tuple[torch.Tensor, torch.Tensor]:
         length = self.length
         if length == 0:

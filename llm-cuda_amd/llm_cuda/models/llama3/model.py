@@ -38,18 +38,37 @@ class Llama3DecoderLayer(nn.Module):
         past_key_value: tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None = None,
         use_cache: bool = False,
     ) -> tuple[torch.Tensor, tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None]:
+        x, mlp_out, present = self.forward_split(
+            x, None, attention_mask=attention_mask, past_key_value=past_key_value,
+            use_cache=use_cache)
+        return x + mlp_out, present
+
+    def forward_split(
+        self,
+        x: torch.Tensor,
+        pending: torch.Tensor | None,
+        attention_mask: torch.Tensor | None = None,
+        past_key_value: tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None = None,
+        use_cache: bool = False,
+    ):
+        """The layer with its last residual add left to the caller.
+
+        The layer's input is x + pending (pending None: x). Returns (x_mid,
+        mlp_out, present) with the layer's output = x_mid + mlp_out, so that a
+        stack can fuse that add with the next layer's input norm. Each add is
+        rounded to x's dtype and normalised exactly as the separate add and
+        norm of the reference layer (model.py:29-42).
+        """
+        norm_in = self.input_layernorm
+        if pending is None:
+            h = norm_in(x)
+        else:
+            h, x = add_rms_norm(x, pending, norm_in.weight, norm_in.eps)
         attn_out, present = self.self_attn(
-            self.input_layernorm(x),
-            attention_mask=attention_mask,
-            past_key_value=past_key_value,
-            use_cache=use_cache,
-        )
-        # x = x + attn_out and its post-attention norm in one HIP pass
-        # (the sum is rounded to x's dtype exactly as the separate add).
-        norm = self.post_attention_layernorm
-        h, x = add_rms_norm(x, attn_out, norm.weight, norm.eps)
-        x = x + self.mlp(h)
-        return x, present
+            h, attention_mask=attention_mask, past_key_value=past_key_value, use_cache=use_cache)
+        norm_post = self.post_attention_layernorm
+        h, x = add_rms_norm(x, attn_out, norm_post.weight, norm_post.eps)
+        return x, self.mlp(h), present
 
 
 class Llama3Model(nn.Module):
@@ -71,16 +90,24 @@ class Llama3Model(nn.Module):
         x = self.embed_tokens(input_ids)
         paged = isinstance(past_key_values, PagedKVCache)
         presents: list[tuple[torch.Tensor, torch.Tensor]] = []
+        # Each layer's closing residual add is fused with the next norm (the
+        # next layer's input norm, or the final norm): `pending` carries the
+        # MLP output still to be added to x.
+        pending: torch.Tensor | None = None
         for idx, layer in enumerate(self.layers):
             if paged:
                 layer_past = past_key_values.get_layer(idx)
             else:
                 layer_past = None if past_key_values is None else past_key_values[idx]
-            x, present = layer(
-                x, attention_mask=attention_mask, past_key_value=layer_past, use_cache=use_cache)
+            x, pending, present = layer.forward_split(
+                x, pending, attention_mask=attention_mask, past_key_value=layer_past,
+                use_cache=use_cache)
             if use_cache and not paged and present is not None:
                 presents.append(present)
-        x = self.norm(x)
+        if pending is None:
+            x = self.norm(x)
+        else:
+            x, _ = add_rms_norm(x, pending, self.norm.weight, self.norm.eps)
         if paged:
             next_cache = past_key_values if use_cache else None
         else:

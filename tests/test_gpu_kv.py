@@ -82,3 +82,56 @@ def test_append_drops_tokens_beyond_capacity_or_bad_pages(cuda):
     assert (kc[0, 0, 2:] == 1).all() and (kc[0, 0, :2] == 0).all()  # seq 0: t=2,3 kept; 4,5 -> page -1
     assert (kc[1] == 0).all() and (kc[3] == 0).all()              # nothing else written
     assert (kc[2] == 0).all()                                     # seq 1 starts in page 99 / beyond
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("S,D", [(1, 64), (3, 128), (2, 20)])
+def test_rope_kv_append_equals_rope_then_append(cuda, dtype, S, D):
+    """The fused decode-time op equals the RoPE kernel followed by the page
+    append and the length update, bit for bit: rotated q, both pools (with a
+    ragged batch, an invalid page entry and strided projection views) and the
+    advanced seq_lens. D = 20 takes the element-wise path."""
+    from llm_cuda.kernels import _ops
+    from llm_cuda.models.llama3.rotary import build_rope_cache
+
+    g = torch.Generator().manual_seed(S * 100 + D)
+    B, Hq, Hkv, P, maxp = 3, 4, 2, 8, 5
+    N = B * maxp + 1
+    table = torch.randperm(N, generator=g)[: B * maxp].to(torch.int32).view(B, maxp)
+    table[2, 3] = -1  # sequence 2: its 4th page is unmapped (tokens dropped)
+    table = table.to(cuda)
+    lens = torch.tensor([0, 7, 23], dtype=torch.int32, device=cuda)
+    pools = [torch.randn(N, Hkv, P, D, generator=g).to(dtype).to(cuda) for _ in range(2)]
+    qkv = torch.randn(B, S, (Hq + 2 * Hkv) * D, generator=g).to(dtype).to(cuda)
+    q = qkv[..., :Hq * D].view(B, S, Hq, D).transpose(1, 2)
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, S, Hkv, D).transpose(1, 2)
+    v = qkv[..., (Hq + Hkv) * D:].view(B, S, Hkv, D).transpose(1, 2)
+    cos, sin = build_rope_cache(maxp * P, D, 10000.0, torch.device(cuda), dtype)
+
+    # separate kernels: per-sequence positions, so rotate each sequence alone
+    ref_k, ref_v = pools[0].clone(), pools[1].clone()
+    ref_q = torch.empty(B, Hq, S, D, dtype=dtype, device=cuda)
+    for b in range(B):
+        p0 = int(lens[b])
+        qb, kb = _ops.rope(q[b:b + 1], cos[p0:p0 + S], sin[p0:p0 + S], k[b:b + 1])
+        ref_q[b] = qb[0]
+        _ops.kv_append(kb, v[b:b + 1], ref_k, ref_v, table[b:b + 1], lens[b:b + 1].clone())
+    got_k, got_v = pools[0].clone(), pools[1].clone()
+    got_lens = lens.clone()
+    got_q = _ops.rope_kv_append(q, k, v, cos, sin, got_k, got_v, table, got_lens)
+    assert torch.equal(_bits(got_q), _bits(ref_q))
+    assert torch.equal(_bits(got_k), _bits(ref_k)) and torch.equal(_bits(got_v), _bits(ref_v))
+    assert torch.equal(got_lens.cpu(), (lens + S).cpu())
+
+
+def test_rope_kv_append_rejects_short_tables(cuda):
+    from llm_cuda.kernels import _ops
+
+    B, H, D, P, maxp = 1, 2, 64, 8, 4
+    pools = [torch.zeros(maxp, H, P, D, device=cuda) for _ in range(2)]
+    table = torch.arange(maxp, dtype=torch.int32, device=cuda).view(1, maxp)
+    x = torch.zeros(B, H, 1, D, device=cuda)
+    cos = torch.zeros(maxp * P - 1, D, device=cuda)
+    with pytest.raises(RuntimeError, match="cover the block-table capacity"):
+        _ops.rope_kv_append(x, x, x, cos, cos, pools[0], pools[1], table,
+                            torch.zeros(1, dtype=torch.int32, device=cuda))
