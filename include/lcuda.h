@@ -113,6 +113,35 @@ LC_API int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void
                         const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
                         float scale, int dtype, void* stream);
 
+/* Bytes of workspace lc_prefill_attn_bwd needs (fp32 delta = rowsum(dO*O)
+ * per query row). */
+LC_API int64_t lc_prefill_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Sq);
+
+/* Causal attention backward with native GQA: given the forward's o and lse
+ * (lc_prefill_attn_fwd) and the output gradient dout, writes
+ *   dq[b,h,i]   = scale * sum_j dS_ij k[b,h/G,j]
+ *   dk[b,g,j]   = scale * sum_{h in group g, i} dS_ij q[b,h,i]
+ *   dv[b,g,j]   =         sum_{h in group g, i} P_ij dout[b,h,i]
+ * with P_ij = exp(q_i.k_j * scale - lse_i) on keys j <= i + q_offset and
+ * dS_ij = P_ij (dout_i.v_j - rowsum(dout_i * o_i)). dq, dk, dv are written,
+ * not accumulated (no atomics; no zero-fill needed).
+ * Replaces kernels/triton/attention.py:181-320 (_fused_causal_attn_bwd) and
+ * :380-454 (_FusedCausalAttentionFunction.backward), which was MHA-only.
+ * q, o, dout, dq: [B, Hq, Sq, D]; k, v, dk, dv: [B, Hkv, Skv, D]; lse fp32
+ * contiguous [B, Hq, Sq]; strides in *_strides[4] (head_dim stride 1).
+ * workspace: >= lc_prefill_attn_bwd_workspace_bytes, 16-byte aligned.
+ * bf16/f16 with D % 8 == 0, D <= 128 run on MFMA; other cases on a generic
+ * fp32-FMA kernel (D <= 256). */
+LC_API int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                        const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D,
+                        const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* v_strides, const int64_t* o_strides,
+                        const int64_t* do_strides, const int64_t* dq_strides,
+                        const int64_t* dk_strides, const int64_t* dv_strides, int64_t q_offset,
+                        float scale, void* workspace, int64_t workspace_bytes, int dtype,
+                        void* stream);
+
 /* Bytes of fp32 workspace lc_paged_decode_fwd needs for these sizes
  * (partial outputs and logsumexps of every split). */
 LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits);

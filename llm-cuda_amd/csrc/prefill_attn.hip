@@ -12,9 +12,12 @@
 
 #include <type_traits>
 
+#include "attn_tiles.h"
 #include "lc_common.h"
 
 namespace {
+
+using namespace lc_attn;
 
 struct PrefillArgs {
   const void* q;
@@ -128,95 +131,10 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 // distinct LDS objects, so the compiler does not make the reads wait for the
 // DMA in flight.
 // ---------------------------------------------------------------------------
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef short i16x8_t __attribute__((ext_vector_type(8)));
-#define LC_LDS __attribute__((address_space(3)))
-
-template <typename T>
-struct Mfma32;
-template <>
-struct Mfma32<bf16_t> {
-  typedef bf16x8_t v8;
-  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma32<f16_t> {
-  typedef f16x8_t v8;
-  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-};
-
 constexpr int kPfWaves = 4;
 constexpr int kPfRows = 32;     // query rows per wave
 constexpr int kPfKeys = 64;     // keys per tile
 constexpr float kPfRescaleLog2 = 8.0f;
-
-// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4],
-// lgkmcnt [11:8]).
-constexpr int kWaitVm0Lgkm0 = 0x0070;  // vmcnt(0) lgkmcnt(0)
-constexpr int kWaitLgkm0 = 0xC07F;     // lgkmcnt(0)
-
-// Workgroup barrier: this wave's LDS reads (and, with WAIT_VM, its DMA) have
-// completed before it arrives.
-template <bool WAIT_VM>
-__device__ __forceinline__ void pf_barrier() {
-  __builtin_amdgcn_s_waitcnt(WAIT_VM ? kWaitVm0Lgkm0 : kWaitLgkm0);
-  lc_compiler_fence();
-  __builtin_amdgcn_s_barrier();
-  lc_compiler_fence();
-}
-
-// LDS swizzle of the prefill K/V tiles: 16-byte chunk c of row r is stored at
-// position c ^ pf_swz(r). Two read patterns must both be bank-conflict free:
-//  * QK^T operands: 16 lanes read one chunk of 16 consecutive rows, so
-//    pf_swz must be a bijection on r mod (rows per bank cycle);
-//  * transposed V^T reads: a 16-lane group reads 4 consecutive rows x 4
-//    consecutive chunks, so 4 consecutive rows must differ in the high
-//    position bits.
-// A plain XOR with r mod 16 fails the second (4 rows map onto the same 4
-// positions); swapping the two 2-bit halves of r mod 16 satisfies both.
-template <int CPR>
-__device__ __forceinline__ int pf_swz(int r) {
-  if constexpr (CPR == 16) {
-    return ((r & 3) << 2) | ((r >> 2) & 3);  // 256-byte rows: one row per bank cycle
-  } else {
-    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);  // 128-byte rows: 2 rows per cycle
-  }
-}
-
-template <int NIW>
-struct PfLoadOffsets {
-  int o[NIW];
-};
-
-// Buffer-to-LDS DMA of one 64-row K or V tile: instruction u of wave w fills
-// LDS rows (w * NIW + u) * RPI .. + RPI - 1 of dst.
-template <int NIW, int RPI, int ROW_B>
-__device__ __forceinline__ void pf_dma_tile(const void* base, int nbytes, LC_LDS char* dst,
-                                            int wave, PfLoadOffsets<NIW> off, int add) {
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
-#pragma unroll
-  for (int u = 0; u < NIW; ++u) {
-    const int row0 = (wave * NIW + u) * RPI;
-    // (a plain local int: the host pass of hipcc rejects this builtin when its
-    // offset operand is a member of a dependent-type parameter)
-    const int vo = off.o[u];
-    // per-lane offset in voffset, the wave-uniform tile offset in soffset
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LC_LDS void*)(dst + row0 * ROW_B), 16, vo, add,
-                                             0, 0);
-  }
-}
-
-// Maximum of x over the two 32-lane halves of the wave (v_permlane32_swap).
-__device__ __forceinline__ float pf_half_max(float x) {
-  const unsigned u = __float_as_uint(x);
-  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-}
 
 template <typename T, int DPAD>
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void

@@ -58,6 +58,13 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p,
          _c_i64p, _c_i64p, _c_i64p, _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
     ),
+    "lc_prefill_attn_bwd_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "lc_prefill_attn_bwd": (
+        ctypes.c_int,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p,
+         _c_i64, ctypes.c_float, _c_p, _c_i64, ctypes.c_int, _c_p],
+    ),
     "lc_paged_decode_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "lc_paged_decode_fwd": (
         ctypes.c_int,

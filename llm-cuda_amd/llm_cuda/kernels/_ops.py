@@ -219,6 +219,53 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offse
     return (out, lse) if return_lse else out
 
 
+def prefill_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                               out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
+                               q_offset: int = 0, scale: float | None = None):
+    """(dq, dk, dv) of causal attention (reference: kernels/triton/attention.py:380-454).
+
+    `out` and `lse` are the forward's output and fp32 natural-log logsumexp.
+    dk and dv are summed over the query heads that share a kv head.
+    """
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [batch, heads, seq, head_dim]")
+    if k.shape != v.shape:
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} shapes differ")
+    B, Hq, Sq, D = q.shape
+    if k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} are incompatible")
+    Hkv, Skv = k.shape[1], k.shape[2]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"n_heads ({Hq}) must be a multiple of n_kv_heads ({Hkv})")
+    if out.shape != q.shape or dout.shape != q.shape:
+        raise ValueError("out and dout must have q's shape")
+    if lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32:
+        raise ValueError("lse must be fp32 [batch, heads, seq]")
+    if not (q.dtype == k.dtype == v.dtype == out.dtype == dout.dtype):
+        raise TypeError("q, k, v, out, dout must share a dtype")
+    dev = nat.require_device(q, k, v, out, lse, dout)
+    q, k, v, out, dout = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v, out, dout))
+    lse = lse.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    dq = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=dev)
+    dk = torch.empty((B, Hkv, Skv, D), dtype=q.dtype, device=dev)
+    dv = torch.empty((B, Hkv, Skv, D), dtype=q.dtype, device=dev)
+    lib = nat.load()
+    ws_bytes = lib.lc_prefill_attn_bwd_workspace_bytes(B, Hq, Sq)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    with _DeviceGuard(dev):
+        rc = lib.lc_prefill_attn_bwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+            dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, Sq, Skv, D,
+            _i64arr(q.stride()), _i64arr(k.stride()), _i64arr(v.stride()),
+            _i64arr(out.stride()), _i64arr(dout.stride()), _i64arr(dq.stride()),
+            _i64arr(dk.stride()), _i64arr(dv.stride()), int(q_offset), float(scale),
+            ws.data_ptr(), ws.numel(), nat.lc_dtype(q), _stream(dev))
+    nat.check(rc, "lc_prefill_attn_bwd")
+    return dq, dk, dv
+
+
 # ---------------------------------------------------------------------------
 # Paged decode  (reference: kernels/triton/decode_attention.py:204-287 over
 # models/llama3/kv_cache.py:65-83)

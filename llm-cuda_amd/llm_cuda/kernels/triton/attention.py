@@ -12,6 +12,11 @@ reference, all widening the accepted inputs:
     prefix (key j is visible to query i iff j <= i + q_offset), the masking of
     models/llama3/attention.py:63-89.
 Additive attention masks are not supported and raise NotImplementedError.
+
+Autograd: when any of q, k, v requires grad, the call goes through
+`_FusedCausalAttentionFunction` (reference: attention.py:323-454), whose
+backward runs lc_prefill_attn_bwd on the saved q, k, v, output and logsumexp.
+The returned lse is not differentiable.
 """
 from __future__ import annotations
 
@@ -49,6 +54,25 @@ def can_use_triton_fused_attention(
     return True
 
 
+class _FusedCausalAttentionFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, q_offset: int):
+        out, lse = _ops.prefill_attention(q, k, v, q_offset=q_offset, return_lse=True)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.q_offset = q_offset
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, out, lse = ctx.saved_tensors
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dq, dk, dv = _ops.prefill_attention_backward(q, k, v, out, lse, dout,
+                                                     q_offset=ctx.q_offset)
+        return dq, dk, dv, None
+
+
 def triton_fused_causal_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -65,4 +89,7 @@ def triton_fused_causal_attention(
             "n_heads a multiple of n_kv_heads")
     if attention_mask is not None:
         raise NotImplementedError("additive attention masks are not supported by the HIP kernel")
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        out, lse = _FusedCausalAttentionFunction.apply(q, k, v, int(q_offset))
+        return (out, lse) if return_lse else out
     return _ops.prefill_attention(q, k, v, q_offset=q_offset, return_lse=return_lse)

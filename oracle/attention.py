@@ -41,3 +41,47 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offset
                 out[b, kvh * G:(kvh + 1) * G, i0:i1] = torch.matmul(p, vv)
                 lse[b, kvh * G:(kvh + 1) * G, i0:i1] = row_lse
     return out, lse
+
+
+def causal_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, do: torch.Tensor,
+                              q_offset: int = 0, scale: float | None = None,
+                              row_chunk: int = 1024):
+    """Gradients of causal_attention's output O with respect to q, k, v, given dO.
+
+    Follows the reference's backward (kernels/triton/attention.py:180-320,
+    380-454): P = exp(s - lse) with s = q k^T * scale (causal), delta =
+    rowsum(dO * O), dP = dO v^T, dS = P * (dP - delta), dq = dS k * scale,
+    dk = dS^T q * scale, dv = P^T dO; under GQA, dk/dv sum over the G query
+    heads that read kv head h // G. Shapes as causal_attention; all fp32.
+    """
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    o, lse = causal_attention(q, k, v, q_offset=q_offset, scale=scale, row_chunk=row_chunk)
+    dq = torch.zeros((B, Hq, Sq, D), dtype=torch.float32)
+    dk = torch.zeros((B, Hkv, Skv, D), dtype=torch.float32)
+    dv = torch.zeros((B, Hkv, Skv, D), dtype=torch.float32)
+    key_pos = torch.arange(Skv).view(1, 1, Skv)
+    for b in range(B):
+        for kvh in range(Hkv):
+            kk = k[b, kvh].float()
+            vv = v[b, kvh].float()
+            hs = slice(kvh * G, (kvh + 1) * G)
+            qg = q[b, hs].float()
+            dog = do[b, hs].float()
+            delta = (dog * o[b, hs]).sum(-1)  # [G, Sq]
+            for i0 in range(0, Sq, row_chunk):
+                i1 = min(Sq, i0 + row_chunk)
+                s = torch.matmul(qg[:, i0:i1], kk.t()) * scale
+                q_pos = torch.arange(i0, i1).view(1, -1, 1) + q_offset
+                row_lse = lse[b, hs, i0:i1].unsqueeze(-1)
+                ok = torch.isfinite(row_lse)
+                p = torch.exp(s - torch.where(ok, row_lse, torch.zeros_like(row_lse)))
+                p = torch.where((key_pos > q_pos) | ~ok, torch.zeros_like(p), p)
+                dp = torch.matmul(dog[:, i0:i1], vv.t())
+                ds = p * (dp - delta[:, i0:i1].unsqueeze(-1))
+                dq[b, hs, i0:i1] = torch.matmul(ds, kk) * scale
+                dk[b, kvh] += torch.einsum("gij,gid->jd", ds, qg[:, i0:i1]) * scale
+                dv[b, kvh] += torch.einsum("gij,gid->jd", p, dog[:, i0:i1])
+    return dq, dk, dv

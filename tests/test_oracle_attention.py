@@ -142,3 +142,71 @@ def test_empty_keys_give_zero_and_neg_inf():
     k = torch.zeros(1, 1, 0, 4)
     o, lse = causal_attention(q, k, k)
     assert (o == 0).all() and torch.isinf(lse).all() and (lse < 0).all()
+
+
+def _autograd_reference(q, k, v, do, q_offset=0):
+    """Independent path: torch autograd through a dense fp64 masked softmax."""
+    G = q.shape[1] // k.shape[1]
+    qd, kd, vd = (t.double().clone().requires_grad_(True) for t in (q, k, v))
+    kr = kd.repeat_interleave(G, dim=1)
+    vr = vd.repeat_interleave(G, dim=1)
+    s = qd @ kr.transpose(-1, -2) / math.sqrt(q.shape[-1])
+    Sq, Skv = q.shape[2], k.shape[2]
+    mask = torch.arange(Skv).view(1, Skv) > (torch.arange(Sq).view(Sq, 1) + q_offset)
+    s = s.masked_fill(mask, float("-inf"))
+    o = torch.softmax(s, -1) @ vr
+    (o * do.double()).sum().backward()
+    return qd.grad, kd.grad, vd.grad
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,off", [(1, 2, 2, 5, 4, 0), (2, 4, 2, 9, 8, 0),
+                                              (1, 4, 1, 7, 16, 3), (2, 3, 3, 16, 32, 0)])
+def test_backward_matches_fp64_autograd(B, Hq, Hkv, S, D, off):
+    from oracle.attention import causal_attention_backward
+
+    g = torch.Generator().manual_seed(S * 10 + D)
+    q = torch.randn(B, Hq, S, D, generator=g)
+    k = torch.randn(B, Hkv, S + off, D, generator=g)
+    v = torch.randn(B, Hkv, S + off, D, generator=g)
+    do = torch.randn(B, Hq, S, D, generator=g)
+    got = causal_attention_backward(q, k, v, do, q_offset=off, row_chunk=4)
+    ref = _autograd_reference(q, k, v, do, q_offset=off)
+    for gt, rf in zip(got, ref):
+        assert (gt.double() - rf).abs().max().item() < 1e-5
+
+
+def test_backward_matches_finite_differences():
+    """dq, dk, dv against central differences of sum(O * dO) in fp64 (tiny shape)."""
+    from oracle.attention import causal_attention, causal_attention_backward
+
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 2, 4, 3, generator=g, dtype=torch.float64)
+    k = torch.randn(1, 1, 4, 3, generator=g, dtype=torch.float64)
+    v = torch.randn(1, 1, 4, 3, generator=g, dtype=torch.float64)
+    do = torch.randn(1, 2, 4, 3, generator=g, dtype=torch.float64)
+
+    def loss(qq, kk, vv):
+        o, _ = causal_attention(qq, kk, vv)
+        return (o.double() * do).sum().item()
+
+    dq, dk, dv = causal_attention_backward(q, k, v, do)
+    eps = 1e-4
+    for t, grad in ((q, dq), (k, dk), (v, dv)):
+        for idx in [(0, 0, 0, 0), (0, 0, 3, 2), (0, t.shape[1] - 1, 2, 1)]:
+            tp, tm = t.clone(), t.clone()
+            tp[idx] += eps
+            tm[idx] -= eps
+            args_p = [tp if x is t else x for x in (q, k, v)]
+            args_m = [tm if x is t else x for x in (q, k, v)]
+            fd = (loss(*args_p) - loss(*args_m)) / (2 * eps)
+            assert abs(fd - grad[idx].item()) < 2e-3 * max(1.0, abs(fd))
+
+
+def test_backward_of_fully_masked_rows_is_zero():
+    """With Skv = 0 nothing is visible: every gradient is zero (no NaN)."""
+    from oracle.attention import causal_attention_backward
+
+    q = torch.randn(1, 2, 3, 8)
+    kv = torch.zeros(1, 1, 0, 8)
+    dq, dk, dv = causal_attention_backward(q, kv, kv, torch.randn(1, 2, 3, 8))
+    assert torch.equal(dq, torch.zeros_like(dq)) and dk.numel() == 0 and dv.numel() == 0
