@@ -7,7 +7,7 @@ step = one paged_decode_attention call (split-K kernel + merge) over all 64
 sequences, inputs resident in HBM. `value` = algorithmic bytes / step time.
 
 Other workloads (--workload): decode70b (config 5), prefill (config 3,
-TFLOP/s), model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
+TFLOP/s), prefill_bwd (the attention backward at the config-3 shape), model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
 swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
 (counter calibration copy).
 
@@ -230,6 +230,62 @@ def run_prefill(args):
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"batch 0, q heads 0-3 / kv head 0 (1/32 of the step), torch fp32 "
                       f"oracle.attention.causal_attention: {secs:.3f} s"}
+    return result
+
+
+def run_prefill_bwd(args):
+    """Causal attention backward at the config-3 prefill shape (a training step's
+    attention backward; the reference's kernels/triton/attention.py:380-454)."""
+    import torch
+
+    from llm_cuda.kernels import _ops
+
+    dev = torch.device("cuda", 0)
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, Hq, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    do = torch.randn(B, Hq, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    out, lse = _ops.prefill_attention(q, k, v, return_lse=True)
+
+    def step():
+        return _ops.prefill_attention_backward(q, k, v, out, lse, do)
+
+    ms, wall = time_steps(step, args.steps, args.warmup)
+    # Algorithmic work: five causal products (S = QK^T recomputed, dP = dO V^T,
+    # dV = P^T dO, dK = dS^T Q, dQ = dS K), each 2 * D flops per visible pair.
+    flops = 5 * B * Hq * D * S * (S + 1)
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"prefill_bwd: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s "
+        f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 dense peak)")
+    result = {
+        "metric": "attention backward throughput",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 5),
+        "dtype": "bf16",
+        "config": {"workload": "causal attention backward (dq, dk, dv), Llama-3-8B prefill "
+                               "shape (BASELINE config 3)",
+                   "batch": B, "seq_len": S, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "kernel": "attention backward (delta + dQ + dK/dV)",
+                     "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic("prefill_attn_bwd_8b")},
+    }
+    if not args.no_cpu_baseline:
+        from oracle.attention import causal_attention_backward
+
+        torch.set_num_threads(cpu_threads())
+        qs, ks, vs, dos = q[:1, :4].cpu(), k[:1, :1].cpu(), v[:1, :1].cpu(), do[:1, :4].cpu()
+        secs = timed_cpu(lambda: causal_attention_backward(qs, ks, vs, dos), budget_s=40.0)
+        sflops = 5 * 1 * 4 * D * S * (S + 1)
+        result["cpu_baseline"] = {
+            "value": round(sflops / secs / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"batch 0, q heads 0-3 / kv head 0 (1/32 of the step), torch fp32 "
+                      f"oracle.attention.causal_attention_backward: {secs:.3f} s"}
     return result
 
 
@@ -523,7 +579,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="decode8b",
-                        choices=["decode8b", "decode70b", "prefill", "model8b", "copycal",
+                        choices=["decode8b", "decode70b", "prefill", "prefill_bwd", "model8b",
+                                 "copycal",
                                  "rmsnorm", "swiglu", "rope"])
     parser.add_argument("--split-tokens", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -550,6 +607,8 @@ def main() -> int:
         res = run_decode(args, decode70b_shape())
     elif args.workload == "prefill":
         res = run_prefill(args)
+    elif args.workload == "prefill_bwd":
+        res = run_prefill_bwd(args)
     elif args.workload == "copycal":
         res = run_copycal(args)
     elif args.workload in ("rmsnorm", "swiglu", "rope"):

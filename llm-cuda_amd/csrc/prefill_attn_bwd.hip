@@ -36,6 +36,7 @@ struct BwdArgs {
   const void* dout;
   const float* lse;    // [B, Hq, Sq], natural log
   const float* delta;  // [B, Hq, Sq]
+  const float* lse2;   // [B, Hq, Sq], lse * log2(e), +inf where lse = -inf
   void* dq;
   void* dk;
   void* dv;
@@ -47,10 +48,14 @@ struct BwdArgs {
 // ---------------------------------------------------------------------------
 // delta = rowsum(dO * O) in fp32: 16 lanes per row.
 // ---------------------------------------------------------------------------
+// Also writes lse2 = lse * log2(e) (+inf for rows that saw no key, so that
+// their probabilities come out as exactly zero) for the MFMA kernels.
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict__ o,
                                                              const T* __restrict__ dout,
+                                                             const float* __restrict__ lse,
                                                              float* __restrict__ delta,
+                                                             float* __restrict__ lse2,
                                                              int64_t os0, int64_t os1,
                                                              int64_t os2, int64_t ds0,
                                                              int64_t ds1, int64_t ds2, int Hq,
@@ -69,7 +74,11 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
   }
 #pragma unroll
   for (int w = 8; w >= 1; w >>= 1) acc += __shfl_xor(acc, w, 64);
-  if (row < rows && sub == 0) delta[row] = acc;
+  if (row < rows && sub == 0) {
+    delta[row] = acc;
+    const float l = lse[row];
+    lse2[row] = l == -INFINITY ? INFINITY : l * kLog2e;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -261,24 +270,553 @@ int launch_bwd_generic(const BwdArgs& a, hipStream_t st) {
   return lc_check_launch("lc_prefill_attn_bwd (generic)");
 }
 
+// ---------------------------------------------------------------------------
+// MFMA kernels (bf16/f16, D a multiple of 8 up to 128, padded to DPAD 64/128).
+//
+// v_mfma_f32_32x32x16 operand layout used throughout: an A operand lane holds
+// row l % 32 and 8 consecutive k; a B operand lane holds column l % 32 and the
+// same 8 k; accumulator register r of lane l holds column l % 32, row
+// 8 (r / 4) + 4 (l / 32) + r % 4. In a product whose B operand is an
+// accumulator of the previous product (P or dS), k index 8 (l / 32) + e is
+// mapped to row 16 jp + 8 (e / 4) + 4 (l / 32) + e % 4 of that accumulator for
+// k-step jp, so a lane's B operand is its own registers 8 jp .. 8 jp + 7; the
+// A operand then comes from ds_read_b64_tr_b16 (4 rows x 16 columns per
+// 16-lane group) over the same rows.
+// ---------------------------------------------------------------------------
+constexpr int kBwWaves = 4;   // dQ kernel: waves per workgroup
+constexpr int kBwRows = 32;   // dQ kernel: query rows per wave
+constexpr int kBwTile = 64;   // rows per LDS tile (keys for dQ, queries for dK/dV)
+constexpr int kBkWaves = 2;   // dK/dV kernel: waves per workgroup (32 keys each)
+
+// LDS offsets shared by both kernels for a tile of 64 rows x DPAD.
+template <int DPAD, int T_SIZE>
+struct TileAddr {
+  static constexpr int KS = DPAD / 16;
+  static constexpr int DTL = DPAD / 32;
+  static constexpr int CPR = DPAD / 8;
+  static constexpr int ROW_B = DPAD * T_SIZE;
+  // Row-major operand reads (ds_read_b128): row l32 (+32 half as an
+  // immediate), chunk hh * CPR/2 + s, i.e. d = hh * DPAD/2 + 8 s .. + 8.
+  int row[KS];
+  // Transposed reads: rows 4hh + te (+8jj, +16jp, +32 half), columns
+  // dt*32 + (gq & 1)*16 + 4tc .. + 4 of each 16-lane group gq.
+  int tr[2][DTL];
+  __device__ __forceinline__ TileAddr(int lane) {
+    const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      row[s] = l32 * ROW_B + (((hh * (CPR / 2) + s) ^ pf_swz<CPR>(l32)) << 4);
+    const int gq = lane >> 4, te = (lane & 15) >> 2, tc = lane & 3;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt) {
+        const int kr = jj * 8 + hh * 4 + te;
+        const int d = dt * 32 + (gq & 1) * 16 + 4 * tc;
+        tr[jj][dt] = kr * ROW_B + ((((d >> 3) ^ pf_swz<CPR>(kr)) << 4) | ((d & 7) * T_SIZE));
+      }
+  }
+};
+
+// Per-lane DMA offsets of a 64-row tile whose rows are `rs` elements apart:
+// instruction u of wave w fills rows (w * NIW + u) * RPI + lane / CPR, chunk
+// position lane % CPR = global chunk ^ pf_swz(row); chunks past head_dim
+// re-read chunk 0 (they meet zero operand elements or land in discarded rows).
+template <int NIW, int DPAD, typename T>
+__device__ __forceinline__ PfLoadOffsets<NIW> tile_dma_offsets(int wave, int lane, int64_t rs,
+                                                               int D) {
+  constexpr int CPR = DPAD / 8, RPI = 64 / CPR;
+  PfLoadOffsets<NIW> off;
+#pragma unroll
+  for (int u = 0; u < NIW; ++u) {
+    const int row = (wave * NIW + u) * RPI + lane / CPR;
+    int ch = (lane % CPR) ^ pf_swz<CPR>(row);
+    ch = ch * 8 < D ? ch : 0;
+    off.o[u] = static_cast<int>(((int64_t)row * rs + ch * 8) * sizeof(T));
+  }
+  return off;
+}
+
+// Row-operand registers: lane holds row `row` (when ok), d = hh*DPAD/2 + 8s.
+template <typename T, int DPAD, typename v8>
+__device__ __forceinline__ void load_row_operand(v8 (&op)[DPAD / 16], const T* rowp, bool ok,
+                                                 int hh, int D) {
+#pragma unroll
+  for (int s = 0; s < DPAD / 16; ++s) {
+    const int d = hh * (DPAD / 2) + s * 8;
+    op[s] = (ok && d < D) ? *reinterpret_cast<const v8*>(rowp + d) : v8{};
+  }
+}
+
+// Store a transposed accumulator (rows d, column = this lane's row of `out`).
+template <typename T, int DTL>
+__device__ __forceinline__ void store_transposed(T* out, const f32x16_t (&acc)[DTL], float mul,
+                                                 int hh, int D) {
+  typedef T t4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = dt * 32 + j * 8 + hh * 4;
+      if (d < D) {
+        t4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = lc_from_f32<T>(acc[dt][j * 4 + i] * mul);
+        *reinterpret_cast<t4*>(out + d) = w;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dQ kernel. Workgroup = 4 waves of 32 query rows sharing one kv head (the
+// forward's grouping: HW = gcd(G, 4) heads x 4 / HW row blocks). Per 64-key
+// tile and wave (keys on accumulator rows, queries on lanes):
+//   S^T  = K  Q^T   (A: K rows from LDS, B: Q^T registers)
+//   dP^T = V  dO^T  (A: V rows from LDS, B: dO^T registers)
+//   dS^T = 2^(S^T scale log2e - lse2) (dP^T - delta)   (per-lane lse2, delta)
+//   dQ^T += K^T dS^T (A: transposed reads of the same K tile, B: dS^T)
+// K and V tiles are double-buffered in LDS and fetched by buffer-to-LDS DMA
+// one tile ahead.
+// ---------------------------------------------------------------------------
+template <typename T, int DPAD>
+__global__ __launch_bounds__(64 * kBwWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
+  typedef Mfma32<T> Ops;
+  typedef typename Ops::v8 v8;
+  typedef TileAddr<DPAD, (int)sizeof(T)> TA;
+  constexpr int KS = TA::KS, DTL = TA::DTL, CPR = TA::CPR, ROW_B = TA::ROW_B;
+  constexpr int RPI = 64 / CPR;
+  constexpr int NIW = kBwTile / (RPI * kBwWaves);
+  constexpr int TILE_B = kBwTile * ROW_B;
+  __shared__ __align__(16) char lds_k0[TILE_B];
+  __shared__ __align__(16) char lds_k1[TILE_B];
+  __shared__ __align__(16) char lds_v0[TILE_B];
+  __shared__ __align__(16) char lds_v1[TILE_B];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+  const int rbw = kBwWaves / hw;
+  const int n_hg = a.G / hw;
+  const int nwg = gridDim.x;
+  const int lin = blockIdx.x;
+  int work = lin;
+  if ((nwg & 7) == 0) work = (lin & 7) * (nwg >> 3) + (lin >> 3);
+  const int unit = work / n_rbg;
+  const int rbg = n_rbg - 1 - (work - unit * n_rbg);
+  const int kvh_hg = unit % (a.Hkv * n_hg);
+  const int b = unit / (a.Hkv * n_hg);
+  const int kvh = kvh_hg / n_hg;
+  const int hgi = kvh_hg - kvh * n_hg;
+  const int head = kvh * a.G + hgi * hw + (wave % hw);
+  const int r0 = (rbg * rbw + wave / hw) * kBwRows;
+  const int wg_last_row = min(a.Sq - 1, (rbg * rbw + rbw) * kBwRows - 1);
+  const int kv_end = min(a.Skv, wg_last_row + a.q_offset + 1);
+  const int my_kv_end = min(a.Skv, min(a.Sq - 1, r0 + kBwRows - 1) + a.q_offset + 1);
+  const int nomask_end = min(a.Skv, r0 + a.q_offset + 1);
+  const bool wave_active = r0 < a.Sq;
+
+  const T* kbase = static_cast<const T*>(a.k) + b * a.ks[0] + (int64_t)kvh * a.ks[1];
+  const T* vbase = static_cast<const T*>(a.v) + b * a.vs[0] + (int64_t)kvh * a.vs[1];
+  const int kbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.ks[2] + a.D) * sizeof(T)) : 0;
+  const int vbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.vs[2] + a.D) * sizeof(T)) : 0;
+
+  const int qi = r0 + l32;
+  const bool row_ok = wave_active && qi < a.Sq;
+  v8 qop[KS], doop[KS];
+  load_row_operand<T, DPAD>(qop, static_cast<const T*>(a.q) + b * a.qs[0] + (int64_t)head * a.qs[1] + (int64_t)qi * a.qs[2], row_ok, hh, a.D);
+  load_row_operand<T, DPAD>(doop, static_cast<const T*>(a.dout) + b * a.dos[0] + (int64_t)head * a.dos[1] + (int64_t)qi * a.dos[2], row_ok, hh, a.D);
+  const int64_t ridx = ((int64_t)b * a.Hq + head) * a.Sq + qi;
+  const float lse2 = row_ok ? a.lse2[ridx] : INFINITY;
+  const float dl = row_ok ? a.delta[ridx] : 0.f;
+
+  const PfLoadOffsets<NIW> koff = tile_dma_offsets<NIW, DPAD, T>(wave, lane, a.ks[2], a.D);
+  const PfLoadOffsets<NIW> voff = tile_dma_offsets<NIW, DPAD, T>(wave, lane, a.vs[2], a.D);
+  const int kstep_b = static_cast<int>(kBwTile * a.ks[2] * sizeof(T));
+  const int vstep_b = static_cast<int>(kBwTile * a.vs[2] * sizeof(T));
+  const TA ad(lane);
+
+  f32x16_t dq[DTL];
+#pragma unroll
+  for (int i = 0; i < DTL; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+  const int n_tiles = (kv_end + kBwTile - 1) / kBwTile;
+
+  auto kbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS char* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS char*)lds_k0;
+    else return (LC_LDS char*)lds_k1;
+  };
+  auto vbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS char* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS char*)lds_v0;
+    else return (LC_LDS char*)lds_v1;
+  };
+
+  auto tile = [&](int t, LC_LDS const char* kl, LC_LDS const char* vl, auto mask_c)
+                  __attribute__((always_inline)) {
+    f32x16_t sa[2], dpa[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sa[kt][r] = 0.f;
+        dpa[kt][r] = 0.f;
+      }
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        sa[kt] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(kl + ad.row[s] + kt * 32 * ROW_B),
+                          qop[s], sa[kt]);
+        dpa[kt] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(vl + ad.row[s] + kt * 32 * ROW_B),
+                           doop[s], dpa[kt]);
+      }
+    v8 dsop[2][2];
+    const int k0 = t * kBwTile;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = fmaf(sa[kt][r], a.scale_log2, -lse2);
+        if constexpr (decltype(mask_c)::value) {
+          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+          if (key > qi + a.q_offset || key >= a.Skv) x = -INFINITY;
+        }
+        const float p = lc_exp2(x);
+        dsop[kt][r >> 3][r & 7] = static_cast<T>(p * (dpa[kt][r] - dl));
+      }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt) {
+          const int rowoff = (kt * 32 + jp * 16) * ROW_B;
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(kl + ad.tr[0][dt] + rowoff));
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(kl + ad.tr[1][dt] + rowoff));
+          const i16x8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          dq[dt] = Ops::mma(__builtin_bit_cast(v8, both), dsop[kt][jp], dq[dt]);
+        }
+  };
+
+  // Iteration t reads tile t from buffers PAR and fetches tile t+1 into the
+  // other pair; the closing barrier publishes it and frees buffers PAR.
+  auto iteration = [&](int t, auto par_c, auto mask_c) __attribute__((always_inline)) {
+    constexpr auto other = std::integral_constant<int, decltype(par_c)::value ^ 1>{};
+    if (t + 1 < n_tiles) {
+      pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(other), wave_s, koff, (t + 1) * kstep_b);
+      pf_dma_tile<NIW, RPI, ROW_B>(vbase, vbytes, vbuf(other), wave_s, voff, (t + 1) * vstep_b);
+    }
+    if (wave_active && t * kBwTile < my_kv_end) tile(t, kbuf(par_c), vbuf(par_c), mask_c);
+    pf_barrier<true>();
+  };
+
+  if (n_tiles > 0) {
+    pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(std::integral_constant<int, 0>{}), wave_s,
+                                 koff, 0);
+    pf_dma_tile<NIW, RPI, ROW_B>(vbase, vbytes, vbuf(std::integral_constant<int, 0>{}), wave_s,
+                                 voff, 0);
+  }
+  pf_barrier<true>();
+  // Leading tiles below every row's diagonal need no mask.
+  const int t_mask = min(n_tiles, nomask_end / kBwTile);
+  const std::integral_constant<int, 0> p0{};
+  const std::integral_constant<int, 1> p1{};
+  int t = 0;
+  for (; t + 1 < t_mask; t += 2) {
+    iteration(t, p0, std::false_type{});
+    iteration(t + 1, p1, std::false_type{});
+  }
+  if (t < t_mask) {
+    iteration(t, p0, std::false_type{});
+    ++t;
+    if (t < n_tiles) {
+      iteration(t, p1, std::true_type{});
+      ++t;
+    }
+  }
+  for (; t < n_tiles; t += 2) {
+    iteration(t, p0, std::true_type{});
+    if (t + 1 >= n_tiles) break;
+    iteration(t + 1, p1, std::true_type{});
+  }
+
+  if (!row_ok) return;
+  store_transposed<T, DTL>(static_cast<T*>(a.dq) + b * a.dqs[0] + (int64_t)head * a.dqs[1] +
+                               (int64_t)qi * a.dqs[2],
+                           dq, a.scale, hh, a.D);
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV kernel. Workgroup = 2 waves of 32 keys (one 64-key block of one kv
+// head); it walks the G query heads of the group and, per head, the 64-row
+// query tiles that see the block. Per tile and wave (queries on accumulator
+// rows, keys on lanes):
+//   S  = Q  K^T   (A: Q rows from LDS, B: K^T registers)
+//   dP = dO V^T   (A: dO rows from LDS, B: V^T registers)
+//   P  = 2^(S scale log2e - lse2),  dS = P (dP - delta)  (lse2, delta per
+//        accumulator row, read from LDS)
+//   dV^T += dO^T P   (A: transposed reads of the dO tile, B: P)
+//   dK^T += Q^T dS   (A: transposed reads of the Q tile, B: dS)
+// Q, dO, lse2 and delta tiles are double-buffered in LDS, fetched by DMA one
+// tile ahead. Blocks are dispatched heaviest (earliest keys) first.
+// ---------------------------------------------------------------------------
+template <typename T, int DPAD>
+__global__ __launch_bounds__(64 * kBkWaves) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+attn_bwd_dkv_mfma_kernel(BwdArgs a, int n_kb) {
+  typedef Mfma32<T> Ops;
+  typedef typename Ops::v8 v8;
+  typedef TileAddr<DPAD, (int)sizeof(T)> TA;
+  constexpr int KS = TA::KS, DTL = TA::DTL, CPR = TA::CPR, ROW_B = TA::ROW_B;
+  constexpr int RPI = 64 / CPR;
+  constexpr int NIW = kBwTile / (RPI * kBkWaves);
+  constexpr int TILE_B = kBwTile * ROW_B;
+  __shared__ __align__(16) char lds_q0[TILE_B];
+  __shared__ __align__(16) char lds_q1[TILE_B];
+  __shared__ __align__(16) char lds_o0[TILE_B];
+  __shared__ __align__(16) char lds_o1[TILE_B];
+  __shared__ __align__(16) float lds_l0[kBwTile];
+  __shared__ __align__(16) float lds_l1[kBwTile];
+  __shared__ __align__(16) float lds_d0[kBwTile];
+  __shared__ __align__(16) float lds_d1[kBwTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+  const int n_units = a.B * a.Hkv;
+  const int kb = blockIdx.x / n_units;
+  const int unit = blockIdx.x - kb * n_units;
+  const int kvh = unit % a.Hkv;
+  const int b = unit / a.Hkv;
+  const int key0 = kb * kBwTile + wave * 32;  // this wave's first key
+  const int kj = key0 + l32;
+  const bool key_ok = kj < a.Skv;
+
+  v8 kop[KS], vop[KS];
+  load_row_operand<T, DPAD>(kop, static_cast<const T*>(a.k) + b * a.ks[0] + (int64_t)kvh * a.ks[1] + (int64_t)kj * a.ks[2], key_ok, hh, a.D);
+  load_row_operand<T, DPAD>(vop, static_cast<const T*>(a.v) + b * a.vs[0] + (int64_t)kvh * a.vs[1] + (int64_t)kj * a.vs[2], key_ok, hh, a.D);
+
+  // Query tiles that see any key of the block: rows i >= kb*64 - q_offset.
+  const int qt0 = max(0, kb * kBwTile - a.q_offset) / kBwTile;
+  const int n_qt = (a.Sq + kBwTile - 1) / kBwTile;
+  const int nq = max(0, n_qt - qt0);
+  const int n_iter = nq * a.G;
+  // Tiles from qt_nomask on see every key of this wave (i + q_offset >= key0 + 31).
+  const int qt_nomask = max(0, key0 + 31 - a.q_offset + kBwTile - 1) / kBwTile;
+
+  const PfLoadOffsets<NIW> qoff = tile_dma_offsets<NIW, DPAD, T>(wave, lane, a.qs[2], a.D);
+  const PfLoadOffsets<NIW> ooff = tile_dma_offsets<NIW, DPAD, T>(wave, lane, a.dos[2], a.D);
+  const int qbytes = a.Sq > 0 ? static_cast<int>(((int64_t)(a.Sq - 1) * a.qs[2] + a.D) * sizeof(T)) : 0;
+  const int obytes = a.Sq > 0 ? static_cast<int>(((int64_t)(a.Sq - 1) * a.dos[2] + a.D) * sizeof(T)) : 0;
+  const int qstep_b = static_cast<int>(kBwTile * a.qs[2] * sizeof(T));
+  const int ostep_b = static_cast<int>(kBwTile * a.dos[2] * sizeof(T));
+  const TA ad(lane);
+
+  f32x16_t dk[DTL], dv[DTL];
+#pragma unroll
+  for (int i = 0; i < DTL; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dk[i][r] = 0.f;
+      dv[i][r] = 0.f;
+    }
+
+  auto qbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS char* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS char*)lds_q0;
+    else return (LC_LDS char*)lds_q1;
+  };
+  auto obuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS char* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS char*)lds_o0;
+    else return (LC_LDS char*)lds_o1;
+  };
+  auto lbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS float* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS float*)lds_l0;
+    else return (LC_LDS float*)lds_l1;
+  };
+  auto dbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS float* {
+    if constexpr (decltype(p_c)::value == 0) return (LC_LDS float*)lds_d0;
+    else return (LC_LDS float*)lds_d1;
+  };
+
+  // DMA of iteration it's tiles (head g = it / nq, query tile qt0 + it % nq).
+  auto fetch = [&](int it, auto p_c) __attribute__((always_inline)) {
+    const int g = it / nq;
+    const int qt = qt0 + (it - g * nq);
+    const int h = kvh * a.G + g;
+    const T* qb = static_cast<const T*>(a.q) + b * a.qs[0] + (int64_t)h * a.qs[1];
+    const T* ob = static_cast<const T*>(a.dout) + b * a.dos[0] + (int64_t)h * a.dos[1];
+    pf_dma_tile<NIW, RPI, ROW_B>(qb, qbytes, qbuf(p_c), wave_s, qoff, qt * qstep_b);
+    pf_dma_tile<NIW, RPI, ROW_B>(ob, obytes, obuf(p_c), wave_s, ooff, qt * ostep_b);
+    // lse2 (wave 0) and delta (wave 1) of the tile's 64 rows: one dword each.
+    const float* src = (wave_s == 0 ? a.lse2 : a.delta) + ((int64_t)b * a.Hq + h) * a.Sq;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(src), 0, a.Sq * 4, 0x00020000);
+    LC_LDS float* dst = wave_s == 0 ? lbuf(p_c) : dbuf(p_c);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LC_LDS void*)dst, 4, lane * 4,
+                                             qt * kBwTile * 4, 0, 0);
+  };
+
+  auto tile = [&](int qt, auto p_c, auto mask_c) __attribute__((always_inline)) {
+    LC_LDS const char* ql = qbuf(p_c);
+    LC_LDS const char* ol = obuf(p_c);
+    LC_LDS const float* ll = lbuf(p_c);
+    LC_LDS const float* dl = dbuf(p_c);
+    f32x16_t sa[2], dpa[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sa[h2][r] = 0.f;
+        dpa[h2][r] = 0.f;
+      }
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        sa[h2] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(ql + ad.row[s] + h2 * 32 * ROW_B),
+                          kop[s], sa[h2]);
+        dpa[h2] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(ol + ad.row[s] + h2 * 32 * ROW_B),
+                           vop[s], dpa[h2]);
+      }
+    v8 pop[2][2], dsop[2][2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = h2 * 32 + j * 8 + hh * 4;
+        const f32x4_t l4 = *reinterpret_cast<LC_LDS const f32x4_t*>(ll + row);
+        const f32x4_t d4 = *reinterpret_cast<LC_LDS const f32x4_t*>(dl + row);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = j * 4 + i;
+          float x = fmaf(sa[h2][r], a.scale_log2, -l4[i]);
+          if constexpr (decltype(mask_c)::value) {
+            if (kj > qt * kBwTile + row + i + a.q_offset) x = -INFINITY;
+          }
+          const float p = lc_exp2(x);
+          pop[h2][r >> 3][r & 7] = static_cast<T>(p);
+          dsop[h2][r >> 3][r & 7] = static_cast<T>(p * (dpa[h2][r] - d4[i]));
+        }
+      }
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt) {
+          const int rowoff = (h2 * 32 + jp * 16) * ROW_B;
+          const i16x4_t olo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(ol + ad.tr[0][dt] + rowoff));
+          const i16x4_t ohi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(ol + ad.tr[1][dt] + rowoff));
+          dv[dt] = Ops::mma(__builtin_bit_cast(v8, __builtin_shufflevector(olo, ohi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                            pop[h2][jp], dv[dt]);
+          const i16x4_t qlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(ql + ad.tr[0][dt] + rowoff));
+          const i16x4_t qhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (LC_LDS i16x4_t*)(ql + ad.tr[1][dt] + rowoff));
+          dk[dt] = Ops::mma(__builtin_bit_cast(v8, __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                            dsop[h2][jp], dk[dt]);
+        }
+  };
+
+  auto iteration = [&](int it, auto par_c) __attribute__((always_inline)) {
+    constexpr auto other = std::integral_constant<int, decltype(par_c)::value ^ 1>{};
+    if (it + 1 < n_iter) fetch(it + 1, other);
+    const int g = it / nq;
+    const int qt = qt0 + (it - g * nq);
+    if (key0 < a.Skv) {
+      if (qt >= qt_nomask)
+        tile(qt, par_c, std::false_type{});
+      else
+        tile(qt, par_c, std::true_type{});
+    }
+    pf_barrier<true>();
+  };
+
+  if (n_iter > 0) fetch(0, std::integral_constant<int, 0>{});
+  pf_barrier<true>();
+  int it = 0;
+  for (; it + 1 < n_iter; it += 2) {
+    iteration(it, std::integral_constant<int, 0>{});
+    iteration(it + 1, std::integral_constant<int, 1>{});
+  }
+  if (it < n_iter) iteration(it, std::integral_constant<int, 0>{});
+
+  if (!key_ok) return;
+  store_transposed<T, DTL>(static_cast<T*>(a.dk) + b * a.dks[0] + (int64_t)kvh * a.dks[1] +
+                               (int64_t)kj * a.dks[2],
+                           dk, a.scale, hh, a.D);
+  store_transposed<T, DTL>(static_cast<T*>(a.dv) + b * a.dvs[0] + (int64_t)kvh * a.dvs[1] +
+                               (int64_t)kj * a.dvs[2],
+                           dv, 1.0f, hh, a.D);
+}
+
+static int gcd_int(int x, int y) {
+  while (y) {
+    const int t = x % y;
+    x = y;
+    y = t;
+  }
+  return x;
+}
+
+template <typename T>
+int launch_bwd_mfma(const BwdArgs& a, hipStream_t st) {
+  const int hw = gcd_int(a.G, kBwWaves);
+  const int rbw = kBwWaves / hw;
+  const int n_rb = (a.Sq + kBwRows - 1) / kBwRows;
+  const int n_rbg = (n_rb + rbw - 1) / rbw;
+  const int64_t nwg_q = (int64_t)n_rbg * a.Hkv * (a.G / hw) * a.B;
+  const int n_kb = (a.Skv + kBwTile - 1) / kBwTile;
+  const int64_t nwg_k = (int64_t)n_kb * a.Hkv * a.B;
+  LC_REQUIRE(nwg_q < (1LL << 31) && nwg_k < (1LL << 31), "lc_prefill_attn_bwd: grid too large");
+  if (nwg_q > 0) {
+    if (a.D <= 64)
+      attn_bwd_dq_mfma_kernel<T, 64><<<(unsigned)nwg_q, 64 * kBwWaves, 0, st>>>(a, hw, n_rbg);
+    else
+      attn_bwd_dq_mfma_kernel<T, 128><<<(unsigned)nwg_q, 64 * kBwWaves, 0, st>>>(a, hw, n_rbg);
+  }
+  if (nwg_k > 0) {
+    if (a.D <= 64)
+      attn_bwd_dkv_mfma_kernel<T, 64><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a, n_kb);
+    else
+      attn_bwd_dkv_mfma_kernel<T, 128><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a, n_kb);
+  }
+  return lc_check_launch("lc_prefill_attn_bwd (mfma)");
+}
+
 template <typename T>
 int launch_delta(const void* o, const int64_t* o_strides, const BwdArgs& a, float* delta,
-                 hipStream_t st) {
+                 float* lse2, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.Hq * a.Sq;
   const int64_t blocks = lc_cdiv(rows * 16, 256);
   LC_REQUIRE(blocks < (1LL << 31), "lc_prefill_attn_bwd: problem too large");
   if (blocks == 0) return LC_OK;
   attn_bwd_delta_kernel<T><<<(unsigned)blocks, 256, 0, st>>>(
-      static_cast<const T*>(o), static_cast<const T*>(a.dout), delta, o_strides[0],
+      static_cast<const T*>(o), static_cast<const T*>(a.dout), a.lse, delta, lse2, o_strides[0],
       o_strides[1], o_strides[2], a.dos[0], a.dos[1], a.dos[2], a.Hq, a.Sq, a.D, rows);
   return lc_check_launch("lc_prefill_attn_bwd (delta)");
 }
 
 template <typename T>
-int run_bwd(const void* o, const int64_t* o_strides, BwdArgs a, float* delta, hipStream_t st) {
-  int rc = launch_delta<T>(o, o_strides, a, delta, st);
+int run_bwd(const void* o, const int64_t* o_strides, BwdArgs a, float* delta, float* lse2,
+            bool mfma, hipStream_t st) {
+  int rc = launch_delta<T>(o, o_strides, a, delta, lse2, st);
   if (rc != LC_OK) return rc;
   a.delta = delta;
+  a.lse2 = lse2;
+  if constexpr (!std::is_same<T, float>::value) {
+    if (mfma) return launch_bwd_mfma<T>(a, st);
+  }
   return launch_bwd_generic<T>(a, st);
 }
 
@@ -288,7 +826,7 @@ extern "C" {
 
 int64_t lc_prefill_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Sq) {
   if (B < 0 || Hq < 0 || Sq < 0) return -1;
-  return ((B * Hq * Sq * 4) + 255) / 256 * 256;
+  return 2 * (((B * Hq * Sq * 4) + 255) / 256 * 256);
 }
 
 int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void* o,
@@ -352,14 +890,27 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
   float* delta = static_cast<float*>(workspace);
+  float* lse2 = delta + need / 8;
+  const int64_t esz = lc_dtype_size(dtype);
+  bool mfma = (dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16) && D % 8 == 0 && D <= 128;
+  for (const void* p : {q, k, v, dout, (const void*)dq, (const void*)dk, (const void*)dv}) mfma = mfma && lc_aligned(p, 16);
+  for (int i = 0; i < 3; ++i)
+    mfma = mfma && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 &&
+           do_strides[i] % 8 == 0 && dq_strides[i] % 8 == 0 && dk_strides[i] % 8 == 0 &&
+           dv_strides[i] % 8 == 0;
+  // Buffer descriptors cover one head's rows with 32-bit byte offsets.
+  mfma = mfma && (Skv * k_strides[2] + D) * esz < (1LL << 31) &&
+         (Skv * v_strides[2] + D) * esz < (1LL << 31) &&
+         (Sq * q_strides[2] + D) * esz < (1LL << 31) &&
+         (Sq * do_strides[2] + D) * esz < (1LL << 31) && Sq * 4 < (1LL << 31);
   hipStream_t st = lc_stream(stream);
   switch (dtype) {
     case LC_DTYPE_F32:
-      return run_bwd<float>(o, o_strides, a, delta, st);
+      return run_bwd<float>(o, o_strides, a, delta, lse2, false, st);
     case LC_DTYPE_BF16:
-      return run_bwd<bf16_t>(o, o_strides, a, delta, st);
+      return run_bwd<bf16_t>(o, o_strides, a, delta, lse2, mfma, st);
     case LC_DTYPE_F16:
-      return run_bwd<f16_t>(o, o_strides, a, delta, st);
+      return run_bwd<f16_t>(o, o_strides, a, delta, lse2, mfma, st);
     default:
       return lc_fail(LC_EINVAL, "lc_prefill_attn_bwd: unknown dtype %d", dtype);
   }

@@ -65,6 +65,9 @@ CASES = [
     (1, 4, 2, 70, 48, torch.bfloat16),
     (1, 2, 1, 33, 256, torch.float32),
     (1, 8, 8, 1, 128, torch.bfloat16),
+    (1, 6, 2, 200, 128, torch.float16),   # G = 3: one head per wave group
+    (2, 16, 2, 129, 64, torch.bfloat16),  # G = 8
+    (1, 2, 2, 64, 96, torch.bfloat16),    # D padded to 128 on the MFMA path
 ]
 
 
