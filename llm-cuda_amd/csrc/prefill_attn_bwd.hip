@@ -50,7 +50,9 @@ struct BwdArgs {
 // ---------------------------------------------------------------------------
 // Also writes lse2 = lse * log2(e) (+inf for rows that saw no key, so that
 // their probabilities come out as exactly zero) for the MFMA kernels.
-template <typename T>
+// 16 lanes per row; VEC: lane c reads elements 8c .. 8c+7 of both rows as one
+// 16-byte load (D a multiple of 8, at most 128).
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict__ o,
                                                              const T* __restrict__ dout,
                                                              const float* __restrict__ lse,
@@ -70,7 +72,17 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const T* __restrict
     const int64_t b = bh / Hq;
     const T* orow = o + b * os0 + h * os1 + (int64_t)i * os2;
     const T* drow = dout + b * ds0 + h * ds1 + (int64_t)i * ds2;
-    for (int d = sub; d < D; d += 16) acc = fmaf(lc_to_f32(orow[d]), lc_to_f32(drow[d]), acc);
+    if constexpr (VEC) {
+      typedef T t8 __attribute__((ext_vector_type(8)));
+      if (sub * 8 < D) {
+        const t8 ov = *reinterpret_cast<const t8*>(orow + sub * 8);
+        const t8 dv = *reinterpret_cast<const t8*>(drow + sub * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf(lc_to_f32(ov[e]), lc_to_f32(dv[e]), acc);
+      }
+    } else {
+      for (int d = sub; d < D; d += 16) acc = fmaf(lc_to_f32(orow[d]), lc_to_f32(drow[d]), acc);
+    }
   }
 #pragma unroll
   for (int w = 8; w >= 1; w >>= 1) acc += __shfl_xor(acc, w, 64);
@@ -286,7 +298,8 @@ int launch_bwd_generic(const BwdArgs& a, hipStream_t st) {
 constexpr int kBwWaves = 4;   // dQ kernel: waves per workgroup
 constexpr int kBwRows = 32;   // dQ kernel: query rows per wave
 constexpr int kBwTile = 64;   // rows per LDS tile (keys for dQ, queries for dK/dV)
-constexpr int kBkWaves = 2;   // dK/dV kernel: waves per workgroup (32 keys each)
+constexpr int kBkWaves = 4;             // dK/dV kernel: waves per workgroup (32 keys each)
+constexpr int kBkKeys = 32 * kBkWaves;  // keys per dK/dV workgroup
 
 // LDS offsets shared by both kernels for a tile of 64 rows x DPAD.
 template <int DPAD, int T_SIZE>
@@ -553,7 +566,7 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV kernel. Workgroup = 2 waves of 32 keys (one 64-key block of one kv
+// dK/dV kernel. Workgroup = 4 waves of 32 keys (one 128-key block of one kv
 // head); it walks the G query heads of the group and, per head, the 64-row
 // query tiles that see the block. Per tile and wave (queries on accumulator
 // rows, keys on lanes):
@@ -596,7 +609,7 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a, int n_kb) {
   const int unit = blockIdx.x - kb * n_units;
   const int kvh = unit % a.Hkv;
   const int b = unit / a.Hkv;
-  const int key0 = kb * kBwTile + wave * 32;  // this wave's first key
+  const int key0 = kb * kBkKeys + wave * 32;  // this wave's first key
   const int kj = key0 + l32;
   const bool key_ok = kj < a.Skv;
 
@@ -604,8 +617,8 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a, int n_kb) {
   load_row_operand<T, DPAD>(kop, static_cast<const T*>(a.k) + b * a.ks[0] + (int64_t)kvh * a.ks[1] + (int64_t)kj * a.ks[2], key_ok, hh, a.D);
   load_row_operand<T, DPAD>(vop, static_cast<const T*>(a.v) + b * a.vs[0] + (int64_t)kvh * a.vs[1] + (int64_t)kj * a.vs[2], key_ok, hh, a.D);
 
-  // Query tiles that see any key of the block: rows i >= kb*64 - q_offset.
-  const int qt0 = max(0, kb * kBwTile - a.q_offset) / kBwTile;
+  // Query tiles that see any key of the block: rows i >= first key - q_offset.
+  const int qt0 = max(0, kb * kBkKeys - a.q_offset) / kBwTile;
   const int n_qt = (a.Sq + kBwTile - 1) / kBwTile;
   const int nq = max(0, n_qt - qt0);
   const int n_iter = nq * a.G;
@@ -646,16 +659,21 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a, int n_kb) {
     else return (LC_LDS float*)lds_d1;
   };
 
-  // DMA of iteration it's tiles (head g = it / nq, query tile qt0 + it % nq).
+  // Iteration it covers query tile n_qt - 1 - it / G of head g = it % G: the
+  // walk runs from the last tile down, so the workgroups of one kv head that
+  // run together read the same Q/dO tiles at about the same time (L2 hits),
+  // and the diagonal tiles that need a mask come last.
   auto fetch = [&](int it, auto p_c) __attribute__((always_inline)) {
-    const int g = it / nq;
-    const int qt = qt0 + (it - g * nq);
+    const int step = it / a.G;
+    const int g = it - step * a.G;
+    const int qt = n_qt - 1 - step;
     const int h = kvh * a.G + g;
     const T* qb = static_cast<const T*>(a.q) + b * a.qs[0] + (int64_t)h * a.qs[1];
     const T* ob = static_cast<const T*>(a.dout) + b * a.dos[0] + (int64_t)h * a.dos[1];
     pf_dma_tile<NIW, RPI, ROW_B>(qb, qbytes, qbuf(p_c), wave_s, qoff, qt * qstep_b);
     pf_dma_tile<NIW, RPI, ROW_B>(ob, obytes, obuf(p_c), wave_s, ooff, qt * ostep_b);
     // lse2 (wave 0) and delta (wave 1) of the tile's 64 rows: one dword each.
+    if (wave_s >= 2) return;
     const float* src = (wave_s == 0 ? a.lse2 : a.delta) + ((int64_t)b * a.Hq + h) * a.Sq;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(src), 0, a.Sq * 4, 0x00020000);
@@ -731,8 +749,7 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a, int n_kb) {
   auto iteration = [&](int it, auto par_c) __attribute__((always_inline)) {
     constexpr auto other = std::integral_constant<int, decltype(par_c)::value ^ 1>{};
     if (it + 1 < n_iter) fetch(it + 1, other);
-    const int g = it / nq;
-    const int qt = qt0 + (it - g * nq);
+    const int qt = n_qt - 1 - it / a.G;
     if (key0 < a.Skv) {
       if (qt >= qt_nomask)
         tile(qt, par_c, std::false_type{});
@@ -776,7 +793,7 @@ int launch_bwd_mfma(const BwdArgs& a, hipStream_t st) {
   const int n_rb = (a.Sq + kBwRows - 1) / kBwRows;
   const int n_rbg = (n_rb + rbw - 1) / rbw;
   const int64_t nwg_q = (int64_t)n_rbg * a.Hkv * (a.G / hw) * a.B;
-  const int n_kb = (a.Skv + kBwTile - 1) / kBwTile;
+  const int n_kb = (a.Skv + kBkKeys - 1) / kBkKeys;
   const int64_t nwg_k = (int64_t)n_kb * a.Hkv * a.B;
   LC_REQUIRE(nwg_q < (1LL << 31) && nwg_k < (1LL << 31), "lc_prefill_attn_bwd: grid too large");
   if (nwg_q > 0) {
@@ -801,7 +818,11 @@ int launch_delta(const void* o, const int64_t* o_strides, const BwdArgs& a, floa
   const int64_t blocks = lc_cdiv(rows * 16, 256);
   LC_REQUIRE(blocks < (1LL << 31), "lc_prefill_attn_bwd: problem too large");
   if (blocks == 0) return LC_OK;
-  attn_bwd_delta_kernel<T><<<(unsigned)blocks, 256, 0, st>>>(
+  bool vec = !std::is_same<T, float>::value && a.D % 8 == 0 && a.D <= 128 &&
+             lc_aligned(o, 16) && lc_aligned(a.dout, 16);
+  for (int i = 0; i < 3; ++i) vec = vec && o_strides[i] % 8 == 0 && a.dos[i] % 8 == 0;
+  auto kern = vec ? attn_bwd_delta_kernel<T, true> : attn_bwd_delta_kernel<T, false>;
+  kern<<<(unsigned)blocks, 256, 0, st>>>(
       static_cast<const T*>(o), static_cast<const T*>(a.dout), a.lse, delta, lse2, o_strides[0],
       o_strides[1], o_strides[2], a.dos[0], a.dos[1], a.dos[2], a.Hq, a.Sq, a.D, rows);
   return lc_check_launch("lc_prefill_attn_bwd (delta)");
