@@ -7,7 +7,8 @@ step = one paged_decode_attention call (split-K kernel + merge) over all 64
 sequences, inputs resident in HBM. `value` = algorithmic bytes / step time.
 
 Other workloads (--workload): decode70b (config 5), prefill (config 3,
-TFLOP/s), prefill_bwd (the attention backward at the config-3 shape), model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
+TFLOP/s), prefill_bwd (the attention backward at the config-3 shape), lm_head
+(fused lm_head + greedy argmax at the config-4 vocab), model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
 swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
 (counter calibration copy).
 
@@ -289,6 +290,65 @@ def run_prefill_bwd(args):
     return result
 
 
+def run_lm_head(args):
+    """Fused lm_head + greedy argmax at the config-4 shape: hidden [32, 4096],
+    weight [128256, 4096] bf16 (reference model.py:156 + :214 at the last position)."""
+    import torch
+
+    from llm_cuda.kernels import _ops
+
+    dev = torch.device("cuda", 0)
+    B, K, V = 32, 4096, 128256
+    g = torch.Generator(device=dev).manual_seed(0)
+    # Two weight copies (2.1 GB) alternate, so no step finds the weight in the
+    # 256 MB Infinity Cache.
+    weights = [(torch.randn(V, K, generator=g, device=dev) * 0.02).bfloat16() for _ in range(2)]
+    hidden = torch.randn(B, K, generator=g, device=dev).bfloat16()
+    state = {"i": 0}
+
+    def step():
+        state["i"] ^= 1
+        return _ops.lm_head_argmax(hidden, weights[state["i"]])
+
+    ms, wall = time_steps(step, args.steps, args.warmup)
+    nbytes = V * K * 2 + B * K * 2 + B * 8
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    def torch_step():
+        state["i"] ^= 1
+        return torch.argmax(torch.nn.functional.linear(hidden, weights[state["i"]]), dim=-1)
+
+    ms_t, _ = time_steps(torch_step, args.steps, args.warmup)
+    log(f"lm_head: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM); "
+        f"hipBLASLt linear + torch.argmax: {ms_t * 1e3:.1f} us")
+    result = {
+        "metric": "lm_head + greedy argmax GB/s",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 5),
+        "dtype": "bf16",
+        "config": {"workload": "fused lm_head + greedy argmax, Llama-3-8B vocab (BASELINE config 4 "
+                               "step tail)", "batch": B, "hidden": K, "vocab": V,
+                   "bytes_per_step": nbytes, "torch_linear_argmax_ms": round(ms_t, 5)},
+        "roofline": {"bound": "hbm", "kernel": "lm_head_argmax_mfma_kernel + reduce",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("lm_head_argmax_8b")},
+    }
+    if not args.no_cpu_baseline:
+        from oracle.lm_head import lm_head_argmax
+
+        torch.set_num_threads(cpu_threads())
+        hs, ws = hidden.cpu(), weights[0].cpu()
+        secs = timed_cpu(lambda: lm_head_argmax(hs, ws), budget_s=40.0)
+        result["cpu_baseline"] = {
+            "value": round(nbytes / secs / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the whole step (32 rows x vocab {V}), oracle.lm_head.lm_head_argmax "
+                      f"(fp64 dot products, rounded to bf16, first-index argmax): {secs:.3f} s"}
+    return result
+
+
 def _model8b_config():
     from llm_cuda.models.llama3.config import Llama3Config
 
@@ -302,7 +362,7 @@ def run_model(args):
     paged KV at context 2048 (seeded random page permutation, pools ~N(0,1)).
 
     The step (embedding, 32 layers of RMSNorm / QKV / RoPE / KV append / paged
-    decode / o_proj / SwiGLU MLP, final norm, lm_head, greedy argmax) is
+    decode / o_proj / SwiGLU MLP, final norm, fused lm_head + greedy argmax) is
     captured once in a HIP graph; the graph starts by resetting every layer's
     seq_lens to 2048, so each replay decodes position 2048 against the same
     cache. The first replay is checked against the eager step.
@@ -339,8 +399,8 @@ def run_model(args):
 
     def step():
         cache.seq_lens_all.fill_(ctx)  # every layer's seq_lens (rows of one tensor)
-        out = model(input_ids=ids, past_key_values=cache, use_cache=True)
-        return torch.argmax(out["logits"][:, -1, :], dim=-1), out["logits"]
+        nxt, _, best = model.greedy_next_token(ids, cache, return_logit=True)
+        return nxt, best
 
     with torch.no_grad():
         reset()
@@ -365,6 +425,14 @@ def run_model(args):
         diff = (g_logits.float() - eager_logits).abs().max().item()
         if not torch.equal(g_ids, eager_ids) or diff > 1e-2:
             raise RuntimeError(f"graph replay differs from eager step (max |dlogit| {diff})")
+        # The fused lm_head + argmax picks the argmax of the full logits.
+        reset()
+        full = model(input_ids=ids, past_key_values=cache, use_cache=True)["logits"][:, -1, :]
+        ref_ids = torch.argmax(full, dim=-1)
+        top = full.float().gather(-1, g_ids.view(-1, 1)).view(-1)
+        ref_top = full.float().gather(-1, ref_ids.view(-1, 1)).view(-1)
+        if ((top - ref_top).abs() > 2.0 ** -7 * ref_top.abs()).any():
+            raise RuntimeError("fused lm_head argmax disagrees with argmax of the logits")
         ms, wall = time_steps(graph.replay, args.steps, args.warmup)
     tok_s = B / (ms * 1e-3)
     weights = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
@@ -580,7 +648,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="decode8b",
                         choices=["decode8b", "decode70b", "prefill", "prefill_bwd", "model8b",
-                                 "copycal",
+                                 "lm_head", "copycal",
                                  "rmsnorm", "swiglu", "rope"])
     parser.add_argument("--split-tokens", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -609,6 +677,8 @@ def main() -> int:
         res = run_prefill(args)
     elif args.workload == "prefill_bwd":
         res = run_prefill_bwd(args)
+    elif args.workload == "lm_head":
+        res = run_lm_head(args)
     elif args.workload == "copycal":
         res = run_copycal(args)
     elif args.workload in ("rmsnorm", "swiglu", "rope"):

@@ -142,6 +142,25 @@ LC_API int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, cons
                         float scale, void* workspace, int64_t workspace_bytes, int dtype,
                         void* stream);
 
+/* Bytes of workspace lc_lm_head_argmax needs (per-block partial maxima). */
+LC_API int64_t lc_lm_head_argmax_workspace_bytes(int64_t B, int64_t V);
+
+/* Greedy next token fused with the lm_head projection:
+ *   ids[b] = argmax_v round(hidden[b, :] . weight[v, :])
+ * round() = the fp32 dot product rounded to `dtype` (the dtype of the logits
+ * the reference compares); NaN ranks highest; ties go to the smallest index
+ * (torch.argmax). max_logit (fp32 [B], may be NULL) receives the winning
+ * rounded logit. The [B, V] logits are never written.
+ * Replaces models/llama3/model.py:156 (self.lm_head(hidden_states)) followed
+ * by model.py:214 (torch.argmax(logits[:, -1, :], dim=-1)) at the last position.
+ * hidden: [B, K] with row stride hidden_row_stride; weight: [V, K] (nn.Linear
+ * layout) with row stride weight_row_stride; ids: int64 [B].
+ * bf16/f16 with K % 128 == 0 run on MFMA; other cases on a generic kernel. */
+LC_API int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight,
+                      int64_t weight_row_stride, int64_t B, int64_t K, int64_t V, int64_t* ids,
+                      float* max_logit, void* workspace, int64_t workspace_bytes, int dtype,
+                      void* stream);
+
 /* Bytes of fp32 workspace lc_paged_decode_fwd needs for these sizes
  * (partial outputs and logsumexps of every split). */
 LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits);

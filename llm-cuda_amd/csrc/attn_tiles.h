@@ -68,9 +68,10 @@ struct PfLoadOffsets {
   int o[NIW];
 };
 
-// Buffer-to-LDS DMA of one 64-row K or V tile: instruction u of wave w fills
-// LDS rows (w * NIW + u) * RPI .. + RPI - 1 of dst.
-template <int NIW, int RPI, int ROW_B>
+// Buffer-to-LDS DMA of one tile: instruction u of wave w fills LDS rows
+// (w * NIW + u) * RPI .. + RPI - 1 of dst. AUX is the loads' cache-policy
+// operand (2 = non-temporal, for data read exactly once).
+template <int NIW, int RPI, int ROW_B, int AUX = 0>
 __device__ __forceinline__ void pf_dma_tile(const void* base, int nbytes, LC_LDS char* dst,
                                             int wave, PfLoadOffsets<NIW> off, int add) {
   const __amdgpu_buffer_rsrc_t rsrc =
@@ -83,7 +84,7 @@ __device__ __forceinline__ void pf_dma_tile(const void* base, int nbytes, LC_LDS
     const int vo = off.o[u];
     // per-lane offset in voffset, the wave-uniform tile offset in soffset
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LC_LDS void*)(dst + row0 * ROW_B), 16, vo, add,
-                                             0, 0);
+                                             0, AUX);
   }
 }
 

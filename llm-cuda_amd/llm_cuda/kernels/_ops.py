@@ -267,6 +267,41 @@ def prefill_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
 
 
 # ---------------------------------------------------------------------------
+# lm_head + greedy argmax  (reference: models/llama3/model.py:156,214)
+# ---------------------------------------------------------------------------
+def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool = False):
+    """ids[b] = argmax_v round(hidden[b] . weight[v]) for hidden [B, K], weight [V, K].
+
+    The logits are rounded to hidden's dtype before the comparison (the
+    reference takes argmax over lm_head's output in the model dtype); NaN
+    ranks highest and ties go to the smallest index, as in torch.argmax.
+    Returns int64 ids [B] (and the winning logits as fp32 [B] with return_max).
+    """
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError(f"hidden {tuple(hidden.shape)} and weight {tuple(weight.shape)} "
+                         "must be [B, K] and [V, K]")
+    if hidden.dtype != weight.dtype:
+        raise TypeError("hidden and weight must share a dtype")
+    dev = nat.require_device(hidden, weight)
+    hidden = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
+    weight = weight if weight.stride(-1) == 1 else weight.contiguous()
+    B, K = hidden.shape
+    V = weight.shape[0]
+    ids = torch.empty(B, dtype=torch.int64, device=dev)
+    mx = torch.empty(B, dtype=torch.float32, device=dev) if return_max else None
+    lib = nat.load()
+    ws_bytes = lib.lc_lm_head_argmax_workspace_bytes(B, V)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    with _DeviceGuard(dev):
+        rc = lib.lc_lm_head_argmax(
+            hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0), B, K, V,
+            ids.data_ptr(), None if mx is None else mx.data_ptr(), ws.data_ptr(), ws.numel(),
+            nat.lc_dtype(hidden), _stream(dev))
+    nat.check(rc, "lc_lm_head_argmax")
+    return (ids, mx) if return_max else ids
+
+
+# ---------------------------------------------------------------------------
 # Paged decode  (reference: kernels/triton/decode_attention.py:204-287 over
 # models/llama3/kv_cache.py:65-83)
 # ---------------------------------------------------------------------------

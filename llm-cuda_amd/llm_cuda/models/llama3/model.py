@@ -14,7 +14,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from llm_cuda.kernels._ops import add_rms_norm
+from llm_cuda.kernels._ops import add_rms_norm, lm_head_argmax
 
 from .attention import Llama3Attention
 from .config import Llama3Config
@@ -181,9 +181,26 @@ class Llama3ForCausalLM(nn.Module):
             past_key_values = None
         cur_input = input_ids
         for _ in range(max_new_tokens):
-            out = self.forward(input_ids=cur_input, past_key_values=past_key_values, use_cache=True)
-            past_key_values = out["past_key_values"]
-            next_token = torch.argmax(out["logits"][:, -1, :], dim=-1, keepdim=True)
+            next_token, past_key_values = self.greedy_next_token(cur_input, past_key_values)
             generated = torch.cat([generated, next_token], dim=1)
             cur_input = next_token
         return generated
+
+    @torch.no_grad()
+    def greedy_next_token(self, input_ids: torch.Tensor, past_key_values=None,
+                          return_logit: bool = False):
+        """argmax of the last position's logits, [B, 1] int64, and the cache.
+
+        The reference computes lm_head over every position and then takes
+        torch.argmax(logits[:, -1, :]) (model.py:156,214); here the lm_head
+        projection and the argmax run as one kernel on the last position only,
+        with the same result (logits rounded to the model dtype, first index on
+        ties) and without writing the [B, V] logits. With return_logit, the
+        winning logit (fp32 [B]) is returned as a third value.
+        """
+        out = self.model(input_ids, past_key_values=past_key_values, use_cache=True)
+        hidden = out["hidden_states"][:, -1, :]
+        ids, best = lm_head_argmax(hidden, self.lm_head.weight, return_max=True)
+        if return_logit:
+            return ids.unsqueeze(-1), out["past_key_values"], best
+        return ids.unsqueeze(-1), out["past_key_values"]

@@ -1,0 +1,111 @@
+"""GPU parity: fused lm_head + greedy argmax vs the oracle (oracle/lm_head.py).
+
+The ids are an index derived from floating-point logits. The GPU sums each dot
+product in fp32 in its own order, so a logit that sits on a rounding boundary
+of the model dtype may round one ulp away from the oracle's fp64 sum. The bar:
+identical ids, except that where they differ the two candidates' exact (fp64)
+logits must lie within one ulp of the model dtype of each other; the number of
+such rows is also bounded. The winning logit must equal the oracle's rounded
+logit at the returned id.
+"""
+import pytest
+import torch
+
+from oracle.lm_head import lm_head_argmax as oracle_argmax
+
+pytestmark = pytest.mark.gpu
+
+# Relative spacing of the model dtype (bf16, f16); for fp32 logits, the
+# accumulated rounding of a K-term fp32 sum in another order (K <= 4096).
+ULP = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 1e-5}
+
+
+def _check(hidden, weight, max_mismatch=0):
+    from llm_cuda.kernels import _ops
+
+    ids, best = _ops.lm_head_argmax(hidden, weight, return_max=True)
+    assert ids.dtype == torch.int64 and ids.shape == (hidden.shape[0],)
+    ref_ids, _, ref_logits = oracle_argmax(hidden, weight)
+    ids_c = ids.cpu()
+    h64 = hidden.detach().cpu().double()
+    w64 = weight.detach().cpu().double()
+    mism = (ids_c != ref_ids).nonzero().view(-1).tolist()
+    assert len(mism) <= max_mismatch, f"{len(mism)} rows differ: {mism[:8]}"
+    for b in mism:
+        a, r = int(ids_c[b]), int(ref_ids[b])
+        la = float(h64[b] @ w64[a])
+        lr = float(h64[b] @ w64[r])
+        tol = ULP[hidden.dtype] * max(abs(lr), 2.0 ** -20)
+        assert abs(la - lr) <= tol, f"row {b}: id {a} ({la}) vs oracle {r} ({lr})"
+    # The winning logit is the rounded logit at the returned id (up to the same
+    # rounding-boundary slack).
+    got = ref_logits.float().gather(-1, ids_c.view(-1, 1)).view(-1)
+    slack = ULP[hidden.dtype] * got.abs().clamp(min=2.0 ** -20)
+    assert ((best.cpu() - got).abs() <= slack).all()
+
+
+@pytest.mark.parametrize("B,K,V,dtype", [
+    (1, 128, 1000, torch.bfloat16),        # one tile, partial last vocab block
+    (5, 256, 4099, torch.bfloat16),
+    (32, 512, 12800, torch.float16),
+    (33, 384, 3000, torch.bfloat16),       # two batch chunks on the MFMA path
+    (70, 128, 515, torch.bfloat16),
+    (3, 200, 777, torch.bfloat16),         # K % 128 != 0: generic kernel
+    (2, 256, 32000, torch.float32),        # config 1 (tiny Llama-3, fp32)
+])
+def test_lm_head_argmax_matches_oracle(cuda, B, K, V, dtype):
+    g = torch.Generator().manual_seed(B * 7 + K)
+    hidden = torch.randn(B, K, generator=g).to(dtype).to(cuda)
+    weight = (torch.randn(V, K, generator=g) * 0.02).to(dtype).to(cuda)
+    _check(hidden, weight)
+
+
+def test_lm_head_argmax_config4_shape(cuda):
+    """Llama-3-8B lm_head (vocab 128256, hidden 4096, bf16), batch 32; weights
+    ~N(0, 0.02) as the model's initialiser, hidden states ~N(0, 1)."""
+    g = torch.Generator(device=cuda).manual_seed(0)
+    hidden = torch.randn(32, 4096, generator=g, device=cuda).bfloat16()
+    weight = (torch.randn(128256, 4096, generator=g, device=cuda) * 0.02).bfloat16()
+    _check(hidden, weight, max_mismatch=1)
+
+
+def test_lm_head_argmax_strided_last_position(cuda):
+    """hidden_states[:, -1, :] of a [B, S, K] tensor (row stride S*K)."""
+    g = torch.Generator().manual_seed(4)
+    hs = torch.randn(6, 9, 256, generator=g).bfloat16().to(cuda)
+    weight = (torch.randn(2000, 256, generator=g) * 0.02).bfloat16().to(cuda)
+    _check(hs[:, -1, :], weight)
+
+
+def test_lm_head_argmax_ties_and_nan(cuda):
+    from llm_cuda.kernels import _ops
+
+    g = torch.Generator().manual_seed(9)
+    K, V = 256, 1000
+    hidden = torch.randn(4, K, generator=g).bfloat16()
+    weight = (torch.randn(V, K, generator=g) * 0.02).bfloat16()
+    winner = oracle_argmax(hidden, weight)[0]
+    # copies of each row's winner at other indices, across workgroup boundaries:
+    # equal logits, so the smallest index of each group must win
+    for b in range(4):
+        weight[900 - b] = weight[winner[b]]
+        weight[130 + b] = weight[winner[b]]
+    expect = oracle_argmax(hidden, weight)[0]
+    assert all(expect[b] <= min(int(winner[b]), 130 + b) for b in range(4))
+    ids = _ops.lm_head_argmax(hidden.to(cuda), weight.to(cuda)).cpu()
+    assert torch.equal(ids, expect)
+    # NaN in a weight row: every batch row picks the first NaN row
+    weight[777] = float("nan")
+    weight[300, 5] = float("nan")
+    ids = _ops.lm_head_argmax(hidden.to(cuda), weight.to(cuda)).cpu()
+    assert ids.tolist() == [300] * 4
+
+
+def test_lm_head_argmax_rejects_bad_shapes(cuda):
+    from llm_cuda.kernels import _ops
+
+    h = torch.zeros(2, 128, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        _ops.lm_head_argmax(h, torch.zeros(10, 64, device=cuda, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        _ops.lm_head_argmax(h, torch.zeros(10, 128, device=cuda, dtype=torch.float16))

@@ -198,3 +198,25 @@ def test_rope_table_cache_is_bit_exact(cuda, dtype):
         rc, rs = build_rope_cache(n, cfg.head_dim, cfg.rope_theta, torch.device(cuda), dtype,
                                   position_offset=past, inv_freq=attn.inv_freq)
         assert torch.equal(cos, rc) and torch.equal(sin, rs)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_greedy_next_token_equals_argmax_of_forward_logits(cuda, dtype):
+    """The fused lm_head + argmax (greedy_next_token) picks the argmax of the
+    forward's last-position logits (reference model.py:156,214), in bf16 and fp32."""
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(5)
+    cfg = _small_config(hidden_size=256, vocab_size=5000)
+    model = Llama3ForCausalLM(cfg).to(device=cuda, dtype=dtype).eval()
+    ids = torch.randint(0, cfg.vocab_size, (3, 10), device=cuda)
+    with torch.no_grad():
+        logits = model(input_ids=ids)["logits"][:, -1, :]
+        nxt, cache, best = model.greedy_next_token(ids, None, return_logit=True)
+    assert nxt.shape == (3, 1) and nxt.dtype == torch.int64 and cache is not None
+    ref = torch.argmax(logits, dim=-1)
+    for b in range(3):
+        a, r = int(nxt[b, 0]), int(ref[b])
+        # equal, or a tie within the logits' rounding
+        assert a == r or abs(float(logits[b, a]) - float(logits[b, r])) <= 2 ** -7 * abs(float(logits[b, r]))
+        assert abs(float(best[b]) - float(logits[b, a])) <= 2 ** -7 * abs(float(logits[b, a])) + 1e-6
