@@ -69,6 +69,18 @@ __device__ __forceinline__ void lc_store16(T* p, const Vec16<T>& x) {
   *reinterpret_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, x);
 }
 
+// Streaming variants with the non-temporal cache-policy bit, for data that is
+// read or written exactly once.
+template <typename T>
+__device__ __forceinline__ Vec16<T> lc_load16_nt(const T* p) {
+  u32x4_t raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return __builtin_bit_cast(Vec16<T>, raw);
+}
+template <typename T>
+__device__ __forceinline__ void lc_store16_nt(T* p, const Vec16<T>& x) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, x), reinterpret_cast<u32x4_t*>(p));
+}
+
 // exp2 on the hardware transcendental unit (v_exp_f32). Input is clamped by the
 // callers' max-subtraction to <= 0, where v_exp_f32 is accurate to ~1 ulp;
 // -inf gives +0.
