@@ -113,8 +113,8 @@ LC_API int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void
                         const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
                         float scale, int dtype, void* stream);
 
-/* Bytes of workspace lc_prefill_attn_bwd needs (fp32 delta = rowsum(dO*O)
- * per query row). */
+/* Bytes of workspace lc_prefill_attn_bwd needs: two fp32 values per query row
+ * (delta = rowsum(dO*O), and lse * log2(e)). */
 LC_API int64_t lc_prefill_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Sq);
 
 /* Causal attention backward with native GQA: given the forward's o and lse
