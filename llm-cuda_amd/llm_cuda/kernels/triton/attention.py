@@ -25,6 +25,43 @@ import torch
 from llm_cuda.kernels import _ops
 
 
+def _select_attention_block_sizes(seq_len: int, head_dim: int) -> tuple[int, int]:
+    """(keys per tile, padded head_dim) of the reference's Triton tiling policy
+    (kernels/triton/attention.py:16-29): 32 / 64 / 128 keys from sequence
+    lengths 256 and 1024 up, head_dim rounded up to a power of two in [16, 128].
+
+    Kept for callers and tests that query it. The HIP kernels do not consult
+    it: the MFMA kernel's tiles are fixed at 64 keys x head_dim padded to 64
+    or 128, the generic kernel's at 16 keys.
+    """
+    if seq_len >= 1024:
+        block_n = 128
+    elif seq_len >= 256:
+        block_n = 64
+    else:
+        block_n = 32
+    block_d = 1 << max(0, int(head_dim) - 1).bit_length()
+    return block_n, min(max(block_d, 16), 128)
+
+
+def _select_attention_num_warps(head_dim: int, block_n: int) -> int:
+    """Warp count of the reference's Triton policy (attention.py:32-38), by the
+    tile's head_dim x keys work: 8 from 8192, 4 from 4096, else 2. Kept for
+    callers that query it; no HIP launch depends on it."""
+    work = int(head_dim) * int(block_n)
+    return 8 if work >= 8192 else (4 if work >= 4096 else 2)
+
+
+def _should_use_cuda_sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          attention_mask: torch.Tensor | None = None) -> bool:
+    """Whether a call would be routed to torch SDPA (reference attention.py:41-58).
+
+    Always False here: this build has no SDPA branch, every eligible call runs
+    the gfx950 MFMA kernel (on host tensors the reference also answers False).
+    """
+    return False
+
+
 def _gqa_compatible(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or k.shape != v.shape:
         return False

@@ -180,3 +180,28 @@ def test_split_heuristic():
     for args in [(1, 1, 1, 1), (3, 5, 7, 1000), (64, 8, 16, 100000)]:
         s = choose_split_tokens(*args)
         assert s % 64 == 0 and 64 <= s <= 1024
+
+
+def test_reference_attention_selectors_are_importable():
+    """test_triton_attention.py:50-76 of the reference, on this package: the
+    tiling helpers keep the reference's policy; SDPA is never selected."""
+    import torch
+
+    from llm_cuda.kernels.triton.attention import (
+        _select_attention_block_sizes,
+        _select_attention_num_warps,
+        _should_use_cuda_sdpa,
+        can_use_triton_fused_attention,
+    )
+
+    assert _select_attention_block_sizes(seq_len=128, head_dim=64) == (32, 64)
+    assert _select_attention_block_sizes(seq_len=512, head_dim=64) == (64, 64)
+    assert _select_attention_block_sizes(seq_len=2048, head_dim=64) == (128, 64)
+    assert _select_attention_block_sizes(seq_len=8, head_dim=5) == (32, 16)
+    assert _select_attention_block_sizes(seq_len=8, head_dim=256) == (32, 128)
+    assert _select_attention_num_warps(64, 128) == 8
+    assert _select_attention_num_warps(64, 64) == 4
+    assert _select_attention_num_warps(16, 32) == 2
+    q = torch.randn(1, 2, 1024, 64, dtype=torch.float16)
+    assert _should_use_cuda_sdpa(q, q, q, attention_mask=None) is False
+    assert can_use_triton_fused_attention(q[:, :, :8, :32], q[:, :, :8, :32], q[:, :, :8, :32]) is False
