@@ -71,11 +71,16 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
 
   float acc = 0.f;
   float cache[ITEMS > 0 ? ITEMS : 1][VEC];
+  // The weights of the cached vectors are loaded up front, with the row, so
+  // the scaling after the reduction waits on no second memory round trip.
+  W wcache[ITEMS > 0 ? ITEMS : 1][VEC];
   if constexpr (ITEMS > 0) {
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int vi = tid + it * nthreads;
       if (vi < nvec) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) wcache[it][e] = w[(int64_t)vi * VEC + e];
         load_row(vi, cache[it]);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc = fmaf(cache[it][e], cache[it][e], acc);
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
         T* dst = yr + (int64_t)vi * VEC;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          const float wv = lc_to_f32(w[(int64_t)vi * VEC + e]);
+          const float wv = lc_to_f32(wcache[it][e]);
           const T rv = lc_from_f32<T>(cache[it][e] * inv_rms * wv);
           if constexpr (VEC * sizeof(T) == 16) {
             out.v[e] = rv;

@@ -35,7 +35,8 @@ using namespace lc_attn;
 constexpr int kLhWaves = 4;
 constexpr int kLhRows = 32 * kLhWaves;  // vocab rows per workgroup
 constexpr int kLhKc = 128;              // hidden columns per tile (256-byte runs per row)
-constexpr int kLhStages = 3;            // LDS ring depth (tiles in flight: stages - 1)
+constexpr int kLhStages = 3;            // LDS ring depth: two tiles in flight
+// (deeper rings, and 64-column tiles, measured no faster)
 // Cache policy of the weight loads: non-temporal. Each weight byte is read
 // once; streaming it past the caches measured 11% faster (230 -> 207 us at
 // the Llama-3-8B vocab) than the default policy. The hidden rows, re-read by
@@ -88,16 +89,10 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   constexpr int H_B = kLhBatch * ROW_B;
   __shared__ __align__(16) char w0[W_B];
   __shared__ __align__(16) char w1[W_B];
-  __shared__ __align__(16) char w2[kLhStages > 2 ? W_B : 16];
-  __shared__ __align__(16) char w3[kLhStages > 3 ? W_B : 16];
-  __shared__ __align__(16) char w4[kLhStages > 4 ? W_B : 16];
-  __shared__ __align__(16) char w5[kLhStages > 5 ? W_B : 16];
+  __shared__ __align__(16) char w2[W_B];
   __shared__ __align__(16) char h0[H_B];
   __shared__ __align__(16) char h1[H_B];
-  __shared__ __align__(16) char h2[kLhStages > 2 ? H_B : 16];
-  __shared__ __align__(16) char h3[kLhStages > 3 ? H_B : 16];
-  __shared__ __align__(16) char h4[kLhStages > 4 ? H_B : 16];
-  __shared__ __align__(16) char h5[kLhStages > 5 ? H_B : 16];
+  __shared__ __align__(16) char h2[H_B];
   __shared__ float red_v[kLhWaves][32];
   __shared__ int red_i[kLhWaves][32];
 
@@ -145,19 +140,13 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
     constexpr int S = decltype(st_c)::value;
     if constexpr (S == 0) return (LC_LDS char*)w0;
     else if constexpr (S == 1) return (LC_LDS char*)w1;
-    else if constexpr (S == 2) return (LC_LDS char*)w2;
-    else if constexpr (S == 3) return (LC_LDS char*)w3;
-    else if constexpr (S == 4) return (LC_LDS char*)w4;
-    else return (LC_LDS char*)w5;
+    else return (LC_LDS char*)w2;
   };
   auto hbuf = [&](auto st_c) __attribute__((always_inline)) -> LC_LDS char* {
     constexpr int S = decltype(st_c)::value;
     if constexpr (S == 0) return (LC_LDS char*)h0;
     else if constexpr (S == 1) return (LC_LDS char*)h1;
-    else if constexpr (S == 2) return (LC_LDS char*)h2;
-    else if constexpr (S == 3) return (LC_LDS char*)h3;
-    else if constexpr (S == 4) return (LC_LDS char*)h4;
-    else return (LC_LDS char*)h5;
+    else return (LC_LDS char*)h2;
   };
   auto fetch = [&](int t, auto st_c) __attribute__((always_inline)) {
     pf_dma_tile<NIW_W, RPI, ROW_B, kLhWeightAux>(wbase, wbytes, wbuf(st_c), wave_s, woff, t * ROW_B);
@@ -178,40 +167,35 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
                             *reinterpret_cast<LC_LDS const v8*>(hl + raddr[s]), acc[s & 1]);
   };
 
-  // Iteration t: wait for tile t (this wave's DMA; the up to NST - 2 tiles
-  // issued after it may still be in flight), barrier (every wave's part of
-  // tile t landed, every wave done with tile t-1), refill tile t-1's stage with
-  // tile t + NST - 1, compute tile t.
+  // Iteration t: wait for tile t (this wave's DMA; tile t+1 may still be in
+  // flight), barrier (every wave's part of tile t landed, every wave done with
+  // tile t-1), refill tile t-1's stage with tile t+2, compute tile t.
+  static_assert(kLhStages == 3, "the loop below is written for a three-stage ring");
   const int n_tiles = a.K / kLhKc;
   constexpr int kNi = NIW_W + NIW_H;  // DMA instructions per wave per tile
-  constexpr int NST = kLhStages;
   auto iteration = [&](int t, auto st_c) __attribute__((always_inline)) {
     constexpr int S = decltype(st_c)::value;
-    const int newer = min(NST - 2, n_tiles - 1 - t);  // tiles issued after tile t
-    switch (newer) {
-      case 4: __builtin_amdgcn_s_waitcnt(lh_waitcnt(4 * kNi, 0)); break;
-      case 3: __builtin_amdgcn_s_waitcnt(lh_waitcnt(3 * kNi, 0)); break;
-      case 2: __builtin_amdgcn_s_waitcnt(lh_waitcnt(2 * kNi, 0)); break;
-      case 1: __builtin_amdgcn_s_waitcnt(lh_waitcnt(kNi, 0)); break;
-      default: __builtin_amdgcn_s_waitcnt(lh_waitcnt(0, 0)); break;
-    }
+    if (t + 1 < n_tiles)
+      __builtin_amdgcn_s_waitcnt(lh_waitcnt(kNi, 0));
+    else
+      __builtin_amdgcn_s_waitcnt(lh_waitcnt(0, 0));
     lc_compiler_fence();
     __builtin_amdgcn_s_barrier();
     lc_compiler_fence();
-    if (t + NST - 1 < n_tiles) fetch(t + NST - 1, std::integral_constant<int, (S + NST - 1) % NST>{});
+    if (t + 2 < n_tiles) fetch(t + 2, std::integral_constant<int, (S + 2) % 3>{});
     compute(st_c);
   };
 
-#define LH_PRE(J) \
-  if constexpr (J < NST - 1) { if (J < n_tiles) fetch(J, std::integral_constant<int, J>{}); }
-#define LH_IT(J) \
-  if constexpr (J < NST) { if (t + J < n_tiles) iteration(t + J, std::integral_constant<int, J>{}); }
-  LH_PRE(0) LH_PRE(1) LH_PRE(2) LH_PRE(3) LH_PRE(4)
-  for (int t = 0; t < n_tiles; t += NST) {
-    LH_IT(0) LH_IT(1) LH_IT(2) LH_IT(3) LH_IT(4) LH_IT(5)
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  fetch(0, I0{});
+  if (n_tiles > 1) fetch(1, I1{});
+  for (int t = 0; t < n_tiles; t += 3) {
+    iteration(t, I0{});
+    if (t + 1 < n_tiles) iteration(t + 1, I1{});
+    if (t + 2 < n_tiles) iteration(t + 2, I2{});
   }
-#undef LH_PRE
-#undef LH_IT
 
   // Epilogue: lane (l32, hh) holds batch row l32 and vocab rows
   // v0 + wave*32 + 8j + 4hh + i for register 4j + i.

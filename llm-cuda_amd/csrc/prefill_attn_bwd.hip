@@ -581,7 +581,7 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
 // ---------------------------------------------------------------------------
 template <typename T, int DPAD>
 __global__ __launch_bounds__(64 * kBkWaves) __attribute__((amdgpu_waves_per_eu(1, 1))) void
-attn_bwd_dkv_mfma_kernel(BwdArgs a, int n_kb) {
+attn_bwd_dkv_mfma_kernel(BwdArgs a) {
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
   typedef TileAddr<DPAD, (int)sizeof(T)> TA;
@@ -804,9 +804,9 @@ int launch_bwd_mfma(const BwdArgs& a, hipStream_t st) {
   }
   if (nwg_k > 0) {
     if (a.D <= 64)
-      attn_bwd_dkv_mfma_kernel<T, 64><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a, n_kb);
+      attn_bwd_dkv_mfma_kernel<T, 64><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a);
     else
-      attn_bwd_dkv_mfma_kernel<T, 128><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a, n_kb);
+      attn_bwd_dkv_mfma_kernel<T, 128><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a);
   }
   return lc_check_launch("lc_prefill_attn_bwd (mfma)");
 }
