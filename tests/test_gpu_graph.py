@@ -1,0 +1,68 @@
+"""HIP-graph capture of a decode step that runs only this library's kernels
+and torch matmuls: paged decode with the fused RoPE + KV append, add + RMSNorm,
+SwiGLU, and the fused lm_head + greedy argmax.
+
+The graph is replayed several times with eager work and synchronisations in
+between; every replay must reproduce the eager step exactly (same ids and the
+same winning logits), which is what a captured serving loop relies on (no
+memset nodes, no host-side state baked into the graph).
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def test_decode_step_graph_replays_match_eager(cuda):
+    from llm_cuda.models.llama3.config import Llama3Config
+    from llm_cuda.models.llama3.kv_cache import PagedKVCache
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    cfg = Llama3Config(vocab_size=3000, hidden_size=256, intermediate_size=512,
+                       num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                       max_position_embeddings=512)
+    torch.manual_seed(0)
+    model = Llama3ForCausalLM(cfg).to(device=cuda, dtype=torch.bfloat16).eval()
+    B, ctx, P = 4, 100, 16
+    cache = PagedKVCache.create(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
+                                256, P, cuda, torch.bfloat16, batch_size=B)
+    g = torch.Generator(device=cuda).manual_seed(0)
+    for layer in cache.layer_caches:
+        layer.key_pages.normal_(generator=g)
+        layer.value_pages.normal_(generator=g)
+    ids = torch.randint(0, cfg.vocab_size, (B, 1), generator=g, device=cuda)
+
+    def reset():
+        cache.seq_lens_all.fill_(ctx)
+        for layer in cache.layer_caches:
+            layer.lengths = [ctx] * B
+
+    def step():
+        cache.seq_lens_all.fill_(ctx)
+        nxt, _, best = model.greedy_next_token(ids, cache, return_logit=True)
+        return nxt, best
+
+    with torch.no_grad():
+        reset()
+        eager_ids, eager_best = (t.clone() for t in step())
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                reset()
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        reset()
+        with torch.cuda.graph(graph):
+            g_ids, g_best = step()
+        for rep in range(4):
+            reset()
+            # unrelated eager work between replays
+            junk = torch.randn(1 << 20, device=cuda).sum()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.isfinite(junk)
+            assert torch.equal(g_ids, eager_ids), f"replay {rep}: ids differ"
+            assert torch.equal(g_best, eager_best), f"replay {rep}: winning logits differ"
