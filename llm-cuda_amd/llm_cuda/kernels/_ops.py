@@ -286,6 +286,11 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
     hidden = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
     weight = weight if weight.stride(-1) == 1 else weight.contiguous()
     B, K = hidden.shape
+    # The MFMA path addresses up to 32 hidden rows with 32-bit byte offsets; a
+    # widely strided view (the last position of a long prompt) is packed first
+    # (B x K elements) rather than sent to the generic kernel.
+    if B > 1 and min(B, 32) * hidden.stride(0) * hidden.element_size() >= 2 ** 31:
+        hidden = hidden.contiguous()
     V = weight.shape[0]
     ids = torch.empty(B, dtype=torch.int64, device=dev)
     mx = torch.empty(B, dtype=torch.float32, device=dev) if return_max else None
