@@ -513,9 +513,12 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
                         const int64_t* q_strides, const int64_t* k_strides,
                         const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
                         float scale, int dtype, void* stream) {
-  LC_REQUIRE(q && k && v && o && q_strides && k_strides && v_strides && o_strides,
-             "lc_prefill_attn_fwd: null pointer");
+  LC_REQUIRE(q_strides && k_strides && v_strides && o_strides,
+             "lc_prefill_attn_fwd: null stride array");
   LC_REQUIRE(B >= 0 && B < 65536 && Sq >= 0 && Skv >= 0, "lc_prefill_attn_fwd: bad shape");
+  // Pointers of empty tensors may be null.
+  LC_REQUIRE((q && o) || B * Sq == 0, "lc_prefill_attn_fwd: null q or o");
+  LC_REQUIRE((k && v) || B * Skv == 0, "lc_prefill_attn_fwd: null k or v");
   LC_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536,
              "lc_prefill_attn_fwd: n_heads (%lld) must be a multiple of n_kv_heads (%lld)",
              (long long)Hq, (long long)Hkv);

@@ -859,12 +859,14 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
                         const int64_t* dk_strides, const int64_t* dv_strides, int64_t q_offset,
                         float scale, void* workspace, int64_t workspace_bytes, int dtype,
                         void* stream) {
-  LC_REQUIRE(q && k && v && o && lse && dout && dq && dk && dv && workspace,
-             "lc_prefill_attn_bwd: null pointer");
   LC_REQUIRE(q_strides && k_strides && v_strides && o_strides && do_strides && dq_strides &&
                  dk_strides && dv_strides,
              "lc_prefill_attn_bwd: null stride array");
   LC_REQUIRE(B >= 0 && B < 65536 && Sq >= 0 && Skv >= 0, "lc_prefill_attn_bwd: bad shape");
+  // Pointers of empty tensors may be null (with Sq == 0, dk and dv are zeroed).
+  LC_REQUIRE((q && o && lse && dout && dq) || B * Sq == 0,
+             "lc_prefill_attn_bwd: null query-side pointer");
+  LC_REQUIRE((k && v && dk && dv) || B * Skv == 0, "lc_prefill_attn_bwd: null key-side pointer");
   LC_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536,
              "lc_prefill_attn_bwd: n_heads (%lld) must be a multiple of n_kv_heads (%lld)",
              (long long)Hq, (long long)Hkv);
@@ -879,6 +881,7 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
   const int64_t need = lc_prefill_attn_bwd_workspace_bytes(B, Hq, Sq);
   LC_REQUIRE(workspace_bytes >= need, "lc_prefill_attn_bwd: workspace %lld < %lld bytes",
              (long long)workspace_bytes, (long long)need);
+  LC_REQUIRE(workspace || need == 0, "lc_prefill_attn_bwd: null workspace");
   LC_REQUIRE(lc_aligned(workspace, 16), "lc_prefill_attn_bwd: workspace not 16-byte aligned");
   if (B == 0 || (Sq == 0 && Skv == 0)) return LC_OK;
 

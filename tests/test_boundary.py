@@ -205,3 +205,21 @@ def test_reference_attention_selectors_are_importable():
     q = torch.randn(1, 2, 1024, 64, dtype=torch.float16)
     assert _should_use_cuda_sdpa(q, q, q, attention_mask=None) is False
     assert can_use_triton_fused_attention(q[:, :, :8, :32], q[:, :, :8, :32], q[:, :, :8, :32]) is False
+
+
+def test_empty_extents_accept_null_pointers():
+    """Empty tensors may carry null data pointers: an empty query set is a no-op,
+    a null pointer behind a non-empty extent is rejected before any launch."""
+    from llm_cuda import _native
+
+    lib = _native.load()
+    st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    rc = lib.lc_prefill_attn_fwd(None, 8, 8, None, None, 1, 4, 2, 0, 16, 64, st, st, st, st, 0,
+                                 1.0, 2, None)
+    assert rc == 0
+    rc = lib.lc_prefill_attn_fwd(None, 8, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, 1.0,
+                                 2, None)
+    assert rc == -1 and b"null q" in lib.lc_last_error()
+    rc = lib.lc_prefill_attn_fwd(8, None, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, 1.0,
+                                 2, None)
+    assert rc == -1 and b"null k" in lib.lc_last_error()

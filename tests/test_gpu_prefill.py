@@ -105,3 +105,15 @@ def test_baseline_prefill_shape_head_subset(cuda):
     ref, ref_lse = causal_attention(qr.cpu(), kr.cpu(), v.cpu())
     assert_close(out, ref, ATOL[torch.bfloat16], "prefill 4096")
     assert_lse_close(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_more_queries_than_keys(cuda, dtype):
+    """Sq > Skv with q_offset 0: rows past the last key see every key."""
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+
+    q, k, v = _qkv(1, 4, 2, 150, 70, 64, dtype, cuda, seed=21)
+    out, lse = triton_fused_causal_attention(q, k, v, return_lse=True)
+    ref, ref_lse = causal_attention(q.cpu(), k.cpu(), v.cpu())
+    assert_close(out, ref, ATOL[dtype], "prefill Sq > Skv")
+    assert_lse_close(lse, ref_lse)

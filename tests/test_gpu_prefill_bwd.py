@@ -137,3 +137,35 @@ def test_no_grad_path_does_not_record_graph(cuda):
     q, k, v, _ = _inputs(1, 2, 2, 8, 8, 64, torch.bfloat16, cuda, seed=2)
     out = triton_fused_causal_attention(q, k, v)
     assert out.grad_fn is None
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_more_queries_than_keys(cuda, dtype):
+    """Sq > Skv with q_offset 0: rows past the last key see every key."""
+    q, k, v, do = _inputs(1, 4, 2, 150, 70, 64, dtype, cuda, seed=21)
+    _check(q, k, v, do, 0, dtype)
+
+
+def test_backward_with_broadcast_output_gradient(cuda):
+    """dO from out.sum(): an expanded, stride-0 gradient."""
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+
+    q, k, v, _ = _inputs(1, 4, 2, 96, 96, 128, torch.bfloat16, cuda, seed=22)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    triton_fused_causal_attention(qg, kg, vg).sum().backward()
+    ones = torch.ones(q.shape, dtype=torch.bfloat16)
+    rdq, rdk, rdv = causal_attention_backward(q.cpu(), k.cpu(), v.cpu(), ones)
+    _assert_grad_close(qg.grad, rdq, torch.bfloat16, "dq")
+    _assert_grad_close(kg.grad, rdk, torch.bfloat16, "dk")
+    _assert_grad_close(vg.grad, rdv, torch.bfloat16, "dv")
+
+
+def test_backward_empty_query_or_key_sets(cuda):
+    from llm_cuda.kernels import _ops
+
+    q, k, v, do = _inputs(1, 2, 2, 0, 16, 64, torch.bfloat16, cuda, seed=23)
+    out, lse = _ops.prefill_attention(q, k, v, return_lse=True)
+    dq, dk, dv = _ops.prefill_attention_backward(q, k, v, out, lse, do)
+    assert dq.shape == q.shape and dk.shape == k.shape
+    # no query row sees any key: dk and dv are zero
+    assert dk.abs().max().item() == 0 and dv.abs().max().item() == 0
