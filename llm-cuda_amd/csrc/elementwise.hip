@@ -407,7 +407,7 @@ int lc_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t 
   LC_REQUIRE(rows >= 0 && hidden > 0, "lc_rmsnorm_fwd: bad shape rows=%lld hidden=%lld",
              (long long)rows, (long long)hidden);
   LC_REQUIRE(hidden < (1LL << 31) && rows < (1LL << 31), "lc_rmsnorm_fwd: shape too large");
-  LC_REQUIRE(x && w && y, "lc_rmsnorm_fwd: null pointer");
+  LC_REQUIRE((x && w && y) || rows == 0, "lc_rmsnorm_fwd: null pointer");
   LC_REQUIRE(w_dtype == dtype || w_dtype == LC_DTYPE_F32,
              "lc_rmsnorm_fwd: weight dtype must equal x dtype or be fp32");
   if (rows == 0) return LC_OK;
@@ -422,10 +422,11 @@ int lc_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void*
   LC_REQUIRE(rows >= 0 && hidden > 0, "lc_add_rmsnorm_fwd: bad shape rows=%lld hidden=%lld",
              (long long)rows, (long long)hidden);
   LC_REQUIRE(hidden < (1LL << 31) && rows < (1LL << 31), "lc_add_rmsnorm_fwd: shape too large");
-  LC_REQUIRE(x && residual && w && y && sum_out, "lc_add_rmsnorm_fwd: null pointer");
+  LC_REQUIRE((x && residual && w && y && sum_out) || rows == 0,
+             "lc_add_rmsnorm_fwd: null pointer");
   LC_REQUIRE(w_dtype == dtype || w_dtype == LC_DTYPE_F32,
              "lc_add_rmsnorm_fwd: weight dtype must equal x dtype or be fp32");
-  LC_REQUIRE(y != sum_out && y != x && y != residual,
+  LC_REQUIRE(rows == 0 || (y != sum_out && y != x && y != residual),
              "lc_add_rmsnorm_fwd: y must not alias x, residual or sum_out");
   if (rows == 0) return LC_OK;
   return dispatch_rmsnorm<true>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, residual,
@@ -437,7 +438,7 @@ int lc_swiglu_fwd(const void* gate, const void* up, void* out, int64_t rows, int
                   int64_t gate_row_stride, int64_t up_row_stride, int64_t out_row_stride,
                   int dtype, void* stream) {
   LC_REQUIRE(rows >= 0 && cols >= 0, "lc_swiglu_fwd: bad shape");
-  LC_REQUIRE(gate && up && out, "lc_swiglu_fwd: null pointer");
+  LC_REQUIRE((gate && up && out) || rows * cols == 0, "lc_swiglu_fwd: null pointer");
   if (rows == 0 || cols == 0) return LC_OK;
   hipStream_t st = lc_stream(stream);
   switch (dtype) {
@@ -463,20 +464,21 @@ int lc_rope_fwd(const void* x1, void* out1, int64_t h1, const int64_t* x1_stride
   LC_REQUIRE(D > 0 && D % 2 == 0, "lc_rope_fwd: head_dim must be even and > 0 (got %lld)",
              (long long)D);
   LC_REQUIRE(B >= 0 && S >= 0 && h1 >= 0 && h2 >= 0, "lc_rope_fwd: bad shape");
-  LC_REQUIRE(x1 && out1 && x1_strides && out1_strides && cos && sin,
-             "lc_rope_fwd: null pointer");
+  if (B * S * (h1 + h2) == 0) return LC_OK;  // nothing to rotate (pointers may be null)
+  LC_REQUIRE(h1 == 0 || (x1 && out1 && x1_strides && out1_strides), "lc_rope_fwd: null pointer");
+  LC_REQUIRE(cos && sin, "lc_rope_fwd: null cos/sin");
   LC_REQUIRE(h2 == 0 || (x2 && out2 && x2_strides && out2_strides),
              "lc_rope_fwd: second tensor incomplete");
-  LC_REQUIRE(x1_strides[3] == 1 && out1_strides[3] == 1 &&
+  LC_REQUIRE((h1 == 0 || (x1_strides[3] == 1 && out1_strides[3] == 1)) &&
                  (h2 == 0 || (x2_strides[3] == 1 && out2_strides[3] == 1)),
              "lc_rope_fwd: head_dim stride must be 1");
-  // With h2 == 0 the grid covers only the rows of tensor 1, so tensor 2 is
-  // never addressed.
+  // The grid covers h1 rows of tensor 1 and h2 of tensor 2, so a tensor with
+  // no heads is never addressed.
   RopeTensor t1{x1, out1, h1, {}, {}};
   RopeTensor t2{x2, out2, h2, {}, {}};
   for (int i = 0; i < 4; ++i) {
-    t1.xs[i] = x1_strides[i];
-    t1.os[i] = out1_strides[i];
+    t1.xs[i] = h1 ? x1_strides[i] : 0;
+    t1.os[i] = h1 ? out1_strides[i] : 0;
     t2.xs[i] = h2 ? x2_strides[i] : 0;
     t2.os[i] = h2 ? out2_strides[i] : 0;
   }

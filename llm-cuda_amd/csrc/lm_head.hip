@@ -339,6 +339,7 @@ int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void*
                       int64_t weight_row_stride, int64_t B, int64_t K, int64_t V, int64_t* ids,
                       float* max_logit, void* workspace, int64_t workspace_bytes, int dtype,
                       void* stream) {
+  if (B == 0) return LC_OK;  // no rows (pointers may be null)
   LC_REQUIRE(hidden && weight && ids && workspace, "lc_lm_head_argmax: null pointer");
   LC_REQUIRE(B >= 0 && B < 65536, "lc_lm_head_argmax: batch %lld out of range", (long long)B);
   LC_REQUIRE(K > 0 && V > 0 && V < (1LL << 31) - kLhGenRows && K < (1LL << 30),

@@ -605,7 +605,8 @@ int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                         int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                         int64_t page_size, int64_t split_tokens, int64_t max_splits, float scale,
                         int dtype, void* stream) {
-  LC_REQUIRE(q && key_pages && value_pages && block_table && seq_lens && out && workspace,
+  LC_REQUIRE((q && key_pages && value_pages && block_table && seq_lens && out && workspace) ||
+                 B == 0,
              "lc_paged_decode_fwd: null pointer");
   LC_REQUIRE(B >= 0 && B < 65536, "lc_paged_decode_fwd: batch %lld out of range", (long long)B);
   LC_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0,

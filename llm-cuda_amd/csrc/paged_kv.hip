@@ -296,10 +296,11 @@ int lc_paged_kv_append(const void* k_new, const void* v_new, const int64_t* k_st
                        const int32_t* block_table, int64_t bt_stride, int64_t max_pages_per_seq,
                        int64_t num_pages, const int32_t* start_pos, int64_t B, int64_t Hkv,
                        int64_t S, int64_t D, int64_t page_size, int dtype, void* stream) {
+  LC_REQUIRE(B >= 0 && S >= 0, "lc_paged_kv_append: bad shape");
+  if (B * S == 0) return LC_OK;  // nothing to append (pointers may be null)
   LC_REQUIRE(k_new && v_new && k_strides && v_strides && key_pages && value_pages &&
                  block_table && start_pos,
              "lc_paged_kv_append: null pointer");
-  LC_REQUIRE(B >= 0 && S >= 0, "lc_paged_kv_append: bad shape");
   LC_REQUIRE(k_strides[3] == 1 && v_strides[3] == 1, "lc_paged_kv_append: head_dim stride != 1");
   int rc = check_pool("lc_paged_kv_append", kv_s_page, kv_s_head, kv_s_tok, max_pages_per_seq,
                       num_pages, bt_stride, page_size, Hkv, D);
@@ -327,9 +328,10 @@ int lc_paged_kv_gather(const void* key_pages, const void* value_pages, int64_t k
                        int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
                        void* k_out, void* v_out, int64_t B, int64_t Hkv, int64_t L, int64_t D,
                        int64_t page_size, int dtype, void* stream) {
+  LC_REQUIRE(B >= 0 && L >= 0, "lc_paged_kv_gather: bad shape");
+  if (B * L == 0) return LC_OK;  // nothing to gather (pointers may be null)
   LC_REQUIRE(key_pages && value_pages && block_table && k_out && v_out,
              "lc_paged_kv_gather: null pointer");
-  LC_REQUIRE(B >= 0 && L >= 0, "lc_paged_kv_gather: bad shape");
   int rc = check_pool("lc_paged_kv_gather", kv_s_page, kv_s_head, kv_s_tok, max_pages_per_seq,
                       num_pages, bt_stride, page_size, Hkv, D);
   if (rc != LC_OK) return rc;
@@ -361,11 +363,12 @@ int lc_rope_kv_append(const void* q, const int64_t* q_strides, const void* k,
                       int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
                       int32_t* seq_lens, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                       int64_t page_size, int dtype, void* stream) {
+  LC_REQUIRE(B >= 0 && B < (1LL << 31) && Hq > 0 && S >= 0 && D > 0 && D % 2 == 0,
+             "lc_rope_kv_append: bad shape");
+  if (B * S == 0) return LC_OK;  // no new tokens (pointers may be null)
   LC_REQUIRE(q && q_strides && k && k_strides && v && v_strides && q_out && q_out_strides &&
                  cos && sin && key_pages && value_pages && block_table && seq_lens,
              "lc_rope_kv_append: null pointer");
-  LC_REQUIRE(B >= 0 && B < (1LL << 31) && Hq > 0 && S >= 0 && D > 0 && D % 2 == 0,
-             "lc_rope_kv_append: bad shape");
   LC_REQUIRE(S * (Hq + 2 * Hkv) * D < (1LL << 30), "lc_rope_kv_append: too many new tokens");
   LC_REQUIRE(q_strides[3] == 1 && k_strides[3] == 1 && v_strides[3] == 1 && q_out_strides[3] == 1,
              "lc_rope_kv_append: head_dim stride must be 1");

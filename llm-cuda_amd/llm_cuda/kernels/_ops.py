@@ -114,6 +114,8 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     if gate.dtype != up.dtype:
         raise TypeError("gate and up must have the same dtype")
     dev = nat.require_device(gate, up)
+    if gate.numel() == 0:
+        return torch.empty(gate.shape, dtype=gate.dtype, device=dev)
     cols = gate.shape[-1] if gate.dim() > 0 else 1
     g2 = gate.reshape(-1, cols)
     u2 = up.reshape(-1, cols)

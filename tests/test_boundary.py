@@ -223,3 +223,24 @@ def test_empty_extents_accept_null_pointers():
     rc = lib.lc_prefill_attn_fwd(8, None, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, 1.0,
                                  2, None)
     assert rc == -1 and b"null k" in lib.lc_last_error()
+
+
+def test_every_entry_accepts_empty_work_with_null_pointers():
+    """Zero rows / tokens / batch: LC_OK without a launch, whatever the pointers."""
+    from llm_cuda import _native
+
+    lib = _native.load()
+    st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    assert lib.lc_rmsnorm_fwd(None, None, None, 0, 8, 8, 8, 1e-5, 2, 2, None) == 0
+    assert lib.lc_add_rmsnorm_fwd(None, None, None, None, None, 0, 8, 8, 8, 8, 8, 1e-5, 2, 2,
+                                  None) == 0
+    assert lib.lc_swiglu_fwd(None, None, None, 0, 8, 8, 8, 8, 2, None) == 0
+    assert lib.lc_rope_fwd(None, None, 1, st, st, None, None, 0, None, None, None, None, 8, 8, 0,
+                           4, 8, 2, None) == 0
+    assert lib.lc_lm_head_argmax(None, 8, None, 8, 0, 8, 8, None, None, None, 0, 2, None) == 0
+    assert lib.lc_prefill_attn_bwd(None, None, None, None, None, None, None, None, None, 0, 4, 2,
+                                   8, 8, 64, st, st, st, st, st, st, st, st, 0, 1.0, None, 0, 2,
+                                   None) == 0
+    # a null pointer behind real work is still an error
+    assert lib.lc_swiglu_fwd(None, None, None, 2, 8, 8, 8, 8, 2, None) == -1
+    assert lib.lc_lm_head_argmax(None, 8, None, 8, 2, 8, 8, None, None, None, 4096, 2, None) == -1
