@@ -244,3 +244,16 @@ def test_every_entry_accepts_empty_work_with_null_pointers():
     # a null pointer behind real work is still an error
     assert lib.lc_swiglu_fwd(None, None, None, 2, 8, 8, 8, 8, 2, None) == -1
     assert lib.lc_lm_head_argmax(None, 8, None, 8, 2, 8, 8, None, None, None, 4096, 2, None) == -1
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """No silent fallback: without the built library every kernel call raises."""
+    import pytest
+
+    from llm_cuda import _native
+
+    monkeypatch.setattr(_native, "_LIB", None)
+    monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "missing" / "liblcuda_hip.so")
+    with pytest.raises(_native.NativeError):
+        _native.load()
+    assert _native.status().startswith("failed")
