@@ -1,6 +1,6 @@
 """Benchmark of the Llama-3 inference attention path on one MI355X.
 
-Default workload: paged GQA flash-decode at Llama-3-8B
+Default workload (benchmark config 2): paged GQA flash-decode at Llama-3-8B
 shape — 64 sequences, 32 q / 8 kv heads, head_dim 128, bf16, contexts
 ~U[512, 8192] (seed 0), 64-token pages in a seeded random permutation. One
 step = one paged_decode_attention call (split-K kernel + merge) over all 64
@@ -46,7 +46,7 @@ def log(msg: str) -> None:
 # ---------------------------------------------------------------------------
 def build_paged(lens, Hq, Hkv, D, P, seed, device):
     """Pools of exactly sum(ceil(len/P)) pages, block table = seeded permutation
-    split in sequence order, padded with -1 (BASELINE config 2/5 construction)."""
+    split in sequence order, padded with -1 (benchmark config 2/5 construction)."""
     import torch
 
     g = torch.Generator().manual_seed(seed)
@@ -358,7 +358,7 @@ def _model8b_config():
 
 
 def run_model(args):
-    """one decode step of random-init Llama-3-8B (bf16), batch 32,
+    """Benchmark config 4: one decode step of random-init Llama-3-8B (bf16), batch 32,
     paged KV at context 2048 (seeded random page permutation, pools ~N(0,1)).
 
     The step (embedding, 32 layers of RMSNorm / QKV / RoPE / KV append / paged
@@ -655,7 +655,7 @@ def main() -> int:
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
-              "the multi-GPU sharding is described in DESIGN.md and not implemented.",
+              "multi-GPU sharding is not implemented.",
               file=sys.stderr)
         return 2
 

@@ -315,7 +315,7 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
 def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens: int) -> int:
     """Tokens per split-K wave.
 
-    512-token splits measured fastest at both BASELINE decode shapes (a split's
+    512-token splits measured fastest at both benchmark decode shapes (a split's
     partial output costs 2 * G * D * 4 bytes of workspace traffic against
     512 * D * 4 bytes of K/V, ~1.6% at G = 8); smaller splits are used only when
     the grid would otherwise leave the 256 CUs idle.

@@ -172,7 +172,7 @@ def test_kv_cache_argument_checks():
 def test_split_heuristic():
     from llm_cuda.kernels._ops import choose_split_tokens
 
-    # both BASELINE decode shapes use 512-token splits
+    # both benchmark decode shapes use 512-token splits
     assert choose_split_tokens(64, 8, 4, 8192) == 512
     assert choose_split_tokens(8, 8, 8, 32768) == 512
     # tiny batch: splits shrink to keep the grid busy, never below 64.

@@ -6,7 +6,7 @@ Cases follow the reference's decode tests (test_triton_decode_attention.py:
 48, batch > 1) and add what paging brings: ragged lengths, random page
 permutations, NaN-poisoned unused slots, invalid table entries, empty
 sequences, page sizes that are not powers of two, split-count invariance, and
-the BASELINE shapes (8B: 32/8 heads, D 128, P 64; 70B: 64/8 heads).
+the benchmark shapes (8B: 32/8 heads, D 128, P 64; 70B: 64/8 heads).
 """
 import math
 
@@ -157,7 +157,7 @@ def test_decode_equals_last_prefill_row(cuda):
 
 
 def test_baseline_8b_shape_subset(cuda):
-    """BASELINE config 2 construction (seed 0, ctx ~ U[512, 8192], P 64, random
+    """Benchmark config 2 construction (seed 0, ctx ~ U[512, 8192], P 64, random
     permutation) on 8 sequences, checked against the oracle."""
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(512, 8193, (8,), generator=g).tolist()
@@ -169,7 +169,7 @@ def test_baseline_8b_shape_subset(cuda):
 
 
 def test_baseline_70b_long_context_subset(cuda):
-    """BASELINE config 5 head layout (64/8 heads, D 128) at context 32768 on 2 sequences."""
+    """Benchmark config 5 head layout (64/8 heads, D 128) at context 32768 on 2 sequences."""
     lens = [32768, 32768 - 37]
     q, kp, vp, bt, sl = _paged_case(lens, 64, 8, 128, 64, torch.bfloat16, cuda, seed=1, poison=False)
     out, lse = _run_paged(q, kp, vp, bt, sl, cuda)

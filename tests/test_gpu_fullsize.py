@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE.json's full sizes.
+"""GPU parity at the benchmark configurations' full sizes.
 
 The oracle cannot recompute a whole config-3 prefill in seconds, so these tests
 compare exactly what it can: every output of config 2 (64 ragged sequences,
@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _config2(device):
-    """BASELINE config 2 as bench.py builds it (seed 0)."""
+    """Benchmark config 2 as bench.py builds it (seed 0)."""
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(512, 8193, (64,), generator=g).tolist()
     P, Hq, Hkv, D = 64, 32, 8, 128

@@ -1,4 +1,4 @@
-"""GPU model-level parity (the harness of BASELINE configs 1 and 4).
+"""GPU model-level parity (the harness of benchmark configs 1 and 4).
 
 * Config 1 (tiny Llama-3, fp32, dim 256, 4 layers, 8/2 heads, FFN 688,
   vocab 32000, batch 2, prompt 64, 16 greedy steps, paged KV with P 64) runs
@@ -111,7 +111,7 @@ def test_chunked_prefill_through_paged_cache(cuda):
 
 
 def test_config1_tiny_llama_greedy_matches_oracle(cuda):
-    """seed 0, fp32, batch 2, prompt 64, 16 greedy steps, paged P 64."""
+    """Benchmark config 1 (tiny Llama-3): seed 0, fp32, batch 2, prompt 64, 16 greedy steps, paged P 64."""
     from llm_cuda.models.llama3.config import Llama3Config
     from llm_cuda.models.llama3.model import Llama3ForCausalLM
 

@@ -2,7 +2,7 @@
 
 Cases follow the reference's attention tests (test_triton_attention.py,
 seeds 0/11) and add native GQA, q_offset (a cached prefix), lengths that are
-not tile multiples, every head_dim the entry accepts, and the BASELINE config-3
+not tile multiples, every head_dim the entry accepts, and the benchmark config-3
 shape (S 4096, 32/8 heads, D 128, RoPE theta 500000) on a head subset.
 """
 import pytest
@@ -88,7 +88,7 @@ def test_reference_extension_entry(cuda):
 
 
 def test_baseline_prefill_shape_head_subset(cuda):
-    """S 4096, D 128, RoPE theta 500000 by the HIP RoPE kernel,
+    """Benchmark config 3: S 4096, D 128, RoPE theta 500000 by the HIP RoPE kernel,
     GQA 4:1; batch 1 and 2 kv-head groups (8 q heads) keep the oracle in seconds."""
     from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
     from llm_cuda.models.llama3.rotary import apply_rotary

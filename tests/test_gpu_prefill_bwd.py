@@ -4,7 +4,7 @@ The oracle (oracle.attention.causal_attention_backward) is pinned against
 fp64 autograd and finite differences in test_oracle_attention.py. Cases follow
 the reference's backward tests (test_triton_attention.py:94-163: fp32
 (2, 3, 8, 16) and f16 (1, 2, 16, 32), seed 11) and add native GQA, q_offset,
-lengths that are not tile multiples, the generic head dims, and a BASELINE-like
+lengths that are not tile multiples, the generic head dims, and a benchmark-like
 head subset.
 
 Tolerance: gradients scale with their own magnitude (a bf16 operand carries a
