@@ -391,6 +391,19 @@ def run_model(args):
         layer.key_pages.normal_(generator=gd)
         layer.value_pages.normal_(generator=gd)
     ids = torch.randint(0, cfg.vocab_size, (B, 1), generator=gd, device=dev)
+    if args.tune_gemms:
+        # The projections stay torch matmuls; PyTorch's TunableOp picks the
+        # fastest hipBLASLt / rocBLAS solution per shape during the first eager
+        # step. A 1 GB rotating buffer keeps the weights out of the 256 MB
+        # Infinity Cache while it times them, as in the real step. Tuning is
+        # switched off again before the graph is captured.
+        import tempfile
+
+        tun = torch.cuda.tunable
+        tun.set_filename(os.path.join(tempfile.gettempdir(), f"lcuda_tunableop_{os.getpid()}.csv"))
+        tun.set_rotating_buffer_size(1024)
+        tun.enable(True)
+        tun.tuning_enable(True)
 
     def reset():
         cache.seq_lens_all.fill_(ctx)
@@ -406,6 +419,8 @@ def run_model(args):
         reset()
         eager_ids, eager_logits = step()
         eager_logits = eager_logits.float().clone()
+        if args.tune_gemms:
+            torch.cuda.tunable.tuning_enable(False)
         # warm the allocator on a side stream, then capture
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -446,7 +461,9 @@ def run_model(args):
         "config": {"workload": "Llama-3-8B decode step, random-init bf16 (BASELINE config 4)",
                    "batch": B, "context": ctx, "page_size": P, "layers": cfg.num_hidden_layers,
                    "hidden": cfg.hidden_size, "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size,
-                   "hip_graph": True, "bytes_per_step": weights + kv},
+                   "hip_graph": True, "bytes_per_step": weights + kv,
+                   "projections": "torch matmul" + (", TunableOp-selected hipBLASLt/rocBLAS "
+                                                    "solutions" if args.tune_gemms else "")},
         "roofline": {"bound": "hbm", "kernel": "whole decode step (weights + KV read once)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
@@ -652,6 +669,8 @@ def main() -> int:
                                  "rmsnorm", "swiglu", "rope"])
     parser.add_argument("--split-tokens", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-gemm-tuning", dest="tune_gemms", action="store_false",
+                        help="model8b: keep torch's default GEMM solutions (no TunableOp)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
