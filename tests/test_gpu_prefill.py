@@ -34,6 +34,8 @@ CASES = [
     (1, 4, 2, 70, 48, torch.bfloat16),    # generic path (D not in {64, 128})
     (1, 2, 1, 33, 256, torch.float32),
     (1, 8, 8, 1, 128, torch.bfloat16),    # single token
+    (1, 16, 2, 200, 128, torch.bfloat16),  # 8 q heads per kv head (70B grouping)
+    (1, 6, 2, 97, 128, torch.float16),     # 3 q heads per kv head
 ]
 
 
@@ -49,13 +51,13 @@ def test_prefill_matches_oracle(cuda, B, Hq, Hkv, S, D, dtype):
     assert_lse_close(lse, ref_lse)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 64), (torch.bfloat16, 128)])
 @pytest.mark.parametrize("Sq,Skv", [(1, 77), (5, 128), (64, 200), (130, 131)])
-def test_prefill_with_cached_prefix(cuda, dtype, Sq, Skv):
+def test_prefill_with_cached_prefix(cuda, dtype, D, Sq, Skv):
     """q_offset = Skv - Sq: the chunked-prefill masking of models/llama3/attention.py:63-89."""
     from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
 
-    q, k, v = _qkv(2, 8, 2, Sq, Skv, 64, dtype, cuda, seed=Sq)
+    q, k, v = _qkv(2, 8, 2, Sq, Skv, D, dtype, cuda, seed=Sq)
     out, lse = triton_fused_causal_attention(q, k, v, return_lse=True, q_offset=Skv - Sq)
     ref, ref_lse = causal_attention(q.cpu(), k.cpu(), v.cpu(), q_offset=Skv - Sq)
     assert_close(out, ref, ATOL[dtype], "prefill offset")
@@ -107,12 +109,12 @@ def test_baseline_prefill_shape_head_subset(cuda):
     assert_lse_close(lse, ref_lse)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_prefill_more_queries_than_keys(cuda, dtype):
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 64), (torch.bfloat16, 128)])
+def test_prefill_more_queries_than_keys(cuda, dtype, D):
     """Sq > Skv with q_offset 0: rows past the last key see every key."""
     from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
 
-    q, k, v = _qkv(1, 4, 2, 150, 70, 64, dtype, cuda, seed=21)
+    q, k, v = _qkv(1, 4, 2, 150, 70, D, dtype, cuda, seed=21)
     out, lse = triton_fused_causal_attention(q, k, v, return_lse=True)
     ref, ref_lse = causal_attention(q.cpu(), k.cpu(), v.cpu())
     assert_close(out, ref, ATOL[dtype], "prefill Sq > Skv")

@@ -77,10 +77,10 @@ def test_backward_matches_oracle(cuda, B, Hq, Hkv, S, D, dtype):
     _check(q, k, v, do, 0, dtype)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 64), (torch.bfloat16, 128)])
 @pytest.mark.parametrize("Sq,Skv", [(1, 77), (5, 128), (64, 200), (130, 131)])
-def test_backward_with_cached_prefix(cuda, dtype, Sq, Skv):
-    q, k, v, do = _inputs(2, 8, 2, Sq, Skv, 64, dtype, cuda, seed=Sq + 3)
+def test_backward_with_cached_prefix(cuda, dtype, D, Sq, Skv):
+    q, k, v, do = _inputs(2, 8, 2, Sq, Skv, D, dtype, cuda, seed=Sq + 3)
     _check(q, k, v, do, Skv - Sq, dtype)
 
 
@@ -139,10 +139,10 @@ def test_no_grad_path_does_not_record_graph(cuda):
     assert out.grad_fn is None
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_backward_more_queries_than_keys(cuda, dtype):
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 64), (torch.bfloat16, 128)])
+def test_backward_more_queries_than_keys(cuda, dtype, D):
     """Sq > Skv with q_offset 0: rows past the last key see every key."""
-    q, k, v, do = _inputs(1, 4, 2, 150, 70, 64, dtype, cuda, seed=21)
+    q, k, v, do = _inputs(1, 4, 2, 150, 70, D, dtype, cuda, seed=21)
     _check(q, k, v, do, 0, dtype)
 
 
