@@ -686,8 +686,10 @@ def main() -> int:
     from llm_cuda import _native
 
     _native.load()
-    log(f"device {torch.cuda.get_device_name(0)}, workload {args.workload}, "
-        f"steps {args.steps}, warmup {args.warmup}")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device {torch.cuda.get_device_name(0)} ({getattr(props, 'gcnArchName', '?')}, "
+        f"{props.multi_processor_count} CUs, {props.total_memory / 2**30:.0f} GiB), "
+        f"workload {args.workload}, steps {args.steps}, warmup {args.warmup}")
     if args.workload == "decode8b":
         res = run_decode(args, decode8b_shape())
     elif args.workload == "decode70b":
