@@ -47,3 +47,20 @@ def assert_lse_close(out: torch.Tensor, ref: torch.Tensor, what: str = "lse") ->
     if fin.any():
         err = ((o[fin] - r[fin]).abs() / r[fin].abs().clamp(min=1.0)).max().item()
         assert err <= LSE_RTOL, f"{what} rel err {err:.3e} > {LSE_RTOL:.0e}"
+
+
+def staircase_qkv(B, Hq, Hkv, Sq, Skv, D, dtype, device, seed, step=6.0):
+    """Scores that jump by `step` (natural-log units, ~8.7 in log2 units) at
+    every 64-key boundary: q rows ~ ones, k_j ~ t_j * ones with t_j rising in
+    steps, plus noise. Every 64-key tile then raises each row's running max by
+    more than the kernels' lazy-rescale threshold (2^8), so the rescale of O and
+    l runs once per tile instead of never (N(0,1) inputs never trigger it past
+    the first tile)."""
+    g = torch.Generator().manual_seed(seed)
+    unit = D ** -0.5 * D  # q . k * scale = t for q = k / t = ones
+    t = step * (torch.arange(Skv) // 64).float() / unit
+    q = (torch.ones(B, Hq, Sq, D) + 0.1 * torch.randn(B, Hq, Sq, D, generator=g)).to(dtype)
+    k = (t[None, None, :, None] * torch.ones(B, Hkv, Skv, D)
+         + 0.3 * torch.randn(B, Hkv, Skv, D, generator=g)).to(dtype)
+    v = torch.randn(B, Hkv, Skv, D, generator=g).to(dtype)
+    return q.to(device), k.to(device), v.to(device)

@@ -8,7 +8,7 @@ shape (S 4096, 32/8 heads, D 128, RoPE theta 500000) on a head subset.
 import pytest
 import torch
 
-from helpers import ATOL, assert_close, assert_lse_close
+from helpers import ATOL, assert_close, assert_lse_close, staircase_qkv
 from oracle.attention import causal_attention
 from oracle.elementwise import apply_rope, build_rope_cache
 
@@ -118,4 +118,26 @@ def test_prefill_more_queries_than_keys(cuda, dtype, D):
     out, lse = triton_fused_causal_attention(q, k, v, return_lse=True)
     ref, ref_lse = causal_attention(q.cpu(), k.cpu(), v.cpu())
     assert_close(out, ref, ATOL[dtype], "prefill Sq > Skv")
+    assert_lse_close(lse, ref_lse)
+
+
+
+@pytest.mark.parametrize("dtype,D,Sq,Skv", [
+    (torch.bfloat16, 128, 300, 300),
+    (torch.float16, 128, 200, 200),
+    (torch.bfloat16, 64, 257, 257),
+    (torch.bfloat16, 128, 70, 390),   # cached prefix: q_offset 320
+    (torch.float32, 128, 150, 150),   # generic kernel
+])
+def test_prefill_running_max_rescales(cuda, dtype, D, Sq, Skv):
+    """The lazy O / l rescale path (a row max growing by more than 2^8)."""
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+
+    q, k, v = staircase_qkv(1, 8, 2, Sq, Skv, D, dtype, cuda, seed=Skv)
+    out, lse = triton_fused_causal_attention(q, k, v, return_lse=True, q_offset=Skv - Sq)
+    ref, ref_lse = causal_attention(q.cpu(), k.cpu(), v.cpu(), q_offset=Skv - Sq)
+    # the construction does move the last rows' maxima up one step per 64 keys
+    # (scores of the first 64 keys are ~0)
+    assert ref_lse.max().item() > 6.0 * ((Skv - 1) // 64) - 1.0
+    assert_close(out, ref, ATOL[dtype], "prefill rescales")
     assert_lse_close(lse, ref_lse)

@@ -14,7 +14,7 @@ with atol the forward's per-dtype bound (bf16 2e-2, f16 1e-2, fp32 1e-4).
 import pytest
 import torch
 
-from helpers import ATOL
+from helpers import ATOL, staircase_qkv
 from oracle.attention import causal_attention_backward
 
 pytestmark = pytest.mark.gpu
@@ -169,3 +169,14 @@ def test_backward_empty_query_or_key_sets(cuda):
     assert dq.shape == q.shape and dk.shape == k.shape
     # no query row sees any key: dk and dv are zero
     assert dk.abs().max().item() == 0 and dv.abs().max().item() == 0
+
+
+@pytest.mark.parametrize("dtype,Sq,Skv", [(torch.bfloat16, 300, 300), (torch.bfloat16, 70, 390),
+                                          (torch.float32, 150, 150)])
+def test_backward_wide_score_range(cuda, dtype, Sq, Skv):
+    """Scores that climb by ~8.7 log2 units every 64 keys (the forward's
+    rescale-path inputs): P spans many orders of magnitude within a row."""
+    q, k, v = staircase_qkv(1, 8, 2, Sq, Skv, 128, dtype, cuda, seed=Skv + 5)
+    g = torch.Generator().manual_seed(Skv)
+    do = torch.randn(q.shape, generator=g).to(dtype).to(cuda)
+    _check(q, k, v, do, Skv - Sq, dtype)
