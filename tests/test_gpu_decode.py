@@ -202,3 +202,31 @@ def test_paged_running_max_rescales(cuda, dtype):
     assert ref_lse.max().item() > 3 * 6.0
     assert_close(out, ref, ATOL[dtype], "paged rescales")
     assert_lse_close(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_paged_lengths_outside_the_table_are_clamped(cuda, dtype):
+    """seq_lens past the block table's capacity read only the table's tokens;
+    a negative length reads none (zeros, lse -inf). Nothing past the table is
+    dereferenced (the pools' free slots are NaN)."""
+    lens = [130, 64, 200]
+    q, kp, vp, bt, sl = _paged_case(lens, 8, 2, 128, 64, dtype, cuda, seed=21, poison=False,
+                                    extra_pages=0)
+    cap = bt.shape[1] * 64
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    # rows 0 and 2 read every token of the pages their table row holds (the row is
+    # padded with -1 past the sequence's pages, and those entries drop out)
+    sl_bad = torch.tensor([cap + 1000, 64, 1 << 30], dtype=torch.int32)
+    out, lse = _run_paged(q, kp, vp, bt, sl_bad, cuda)
+    assert_close(out[1:2], ref[1:2], ATOL[dtype], "in-range row")
+    assert_lse_close(lse[1:2], ref_lse[1:2])
+    for b in (0, 2):
+        own = int((bt[b] >= 0).sum())
+        kk = torch.cat([kp[int(bt[b, i])] for i in range(own)], dim=1)[None]
+        vv = torch.cat([vp[int(bt[b, i])] for i in range(own)], dim=1)[None]
+        r, rl = decode_attention(q[b:b + 1], kk, vv)
+        assert_close(out[b:b + 1], r, ATOL[dtype], f"clamped row {b}")
+        assert_lse_close(lse[b:b + 1], rl)
+    out, lse = _run_paged(q, kp, vp, bt, torch.tensor([-7, 64, 0], dtype=torch.int32), cuda)
+    assert (out[0].float().cpu() == 0).all() and torch.isinf(lse[0].cpu()).all()
+    assert (out[2].float().cpu() == 0).all() and torch.isinf(lse[2].cpu()).all()
