@@ -4,7 +4,6 @@ Two tiers (as in the reference's tests): CPU tests run everywhere and cover the
 oracle, host-side logic and the C ABI boundary; tests marked `gpu` run the HIP
 kernels on a ROCm device and compare them with the oracle.
 """
-import os
 import sys
 from pathlib import Path
 
