@@ -14,7 +14,9 @@ swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
 
 Prints one JSON line with the driver's fields plus `roofline` (the dominant
 kernel against MI355X peaks) and `cpu_baseline` (the CPU oracle on the host
-cores, bounded sample).
+cores, bounded sample). The default run also measures the metric's other two
+figures, prefill TFLOP/s (config 3) and decode tok/s (config 4), and adds them
+under `secondary` (`--no-secondary` skips them).
 """
 from __future__ import annotations
 
@@ -671,6 +673,9 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gemm-tuning", dest="tune_gemms", action="store_false",
                         help="model8b: keep torch's default GEMM solutions (no TunableOp)")
+    parser.add_argument("--no-secondary", dest="secondary", action="store_false",
+                        help="decode8b: skip the prefill (config 3) and decode-step (config 4) "
+                             "figures added to the line under 'secondary'")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
@@ -715,8 +720,38 @@ def main() -> int:
     }
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]
+    if args.workload == "decode8b" and args.secondary:
+        line["secondary"] = run_secondary(args)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def run_secondary(args) -> dict:
+    """The metric's other two figures, measured in the same run after the primary
+    one: prefill attention TFLOP/s at config 3 and decode tok/s at config 4 (same
+    steps and warm-up; no CPU baselines, which `--workload prefill` and
+    `--workload model8b` report). A failure is recorded, not raised, so the
+    primary line is still printed."""
+    import copy
+    import gc
+
+    import torch
+
+    sub = copy.copy(args)
+    sub.no_cpu_baseline = True
+    out = {}
+    for key, fn in (("prefill_config3", run_prefill), ("decode_step_config4", run_model)):
+        try:
+            r = fn(sub)
+            out[key] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+                        "workload": r["config"]["workload"],
+                        "frac_of_peak": r["roofline"]["frac"],
+                        "peak": f"{r['roofline']['peak']} {r['roofline']['unit']}"}
+        except Exception as exc:  # recorded in the line
+            out[key] = {"error": f"{type(exc).__name__}: {exc}"}
+        gc.collect()
+        torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":
