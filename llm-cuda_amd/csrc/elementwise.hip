@@ -292,28 +292,34 @@ struct RopeTensor {
   int64_t os[4];
 };
 
-template <typename T, int VEC>
+// I: index type of the row decomposition. 32-bit unsigned division is a short
+// reciprocal sequence; 64-bit division is a long expansion that measurably
+// slows this HBM-bound kernel, so it is used only for grids of 2^32 lanes or
+// more.
+template <typename T, int VEC, typename I>
 __global__ __launch_bounds__(256) void rope_kernel(RopeTensor t1, RopeTensor t2,
                                                    const T* __restrict__ cos,
                                                    const T* __restrict__ sin, int64_t cs_s,
                                                    int64_t sn_s, int S, int half,
                                                    int64_t rows1, int64_t rows_total) {
-  const int chunks = half / VEC;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = gid / chunks;
-  if (row >= rows_total) return;
+  const I chunks = static_cast<I>(half / VEC);
+  const I gid = static_cast<I>(blockIdx.x) * static_cast<I>(blockDim.x) + threadIdx.x;
+  const I row = gid / chunks;
+  if (row >= static_cast<I>(rows_total)) return;
   const int d0 = static_cast<int>(gid - row * chunks) * VEC;
 
-  const bool second = row >= rows1;
+  const bool second = row >= static_cast<I>(rows1);
   const RopeTensor& t = second ? t2 : t1;
-  const int64_t r = second ? row - rows1 : row;
+  const I r = second ? row - static_cast<I>(rows1) : row;
   // Rows are ordered (b, s, h), heads fastest: neighbouring rows share one
   // cos/sin row (served from L1 after the first), and for activations laid
   // out as [B, S, H, D] projection views they are also adjacent in memory.
-  const int64_t h = r % t.h;
-  const int64_t bs = r / t.h;
-  const int s = static_cast<int>(bs % S);
-  const int64_t b = bs / S;
+  const I nh = static_cast<I>(t.h);
+  const I bs = r / nh;
+  const int64_t h = static_cast<int64_t>(r - bs * nh);
+  const I bi = bs / static_cast<I>(S);
+  const int s = static_cast<int>(bs - bi * static_cast<I>(S));
+  const int64_t b = static_cast<int64_t>(bi);
 
   const T* xp = static_cast<const T*>(t.x) + b * t.xs[0] + h * t.xs[1] + (int64_t)s * t.xs[2];
   T* op = static_cast<T*>(t.out) + b * t.os[0] + h * t.os[1] + (int64_t)s * t.os[2];
@@ -386,14 +392,23 @@ int launch_rope(const RopeTensor& t1, const RopeTensor& t2, const void* cos, con
   const int64_t blocks = lc_cdiv(threads_total, threads);
   LC_REQUIRE(blocks < (1LL << 31), "lc_rope_fwd: problem too large");
   if (blocks == 0) return LC_OK;
-  if (vec_ok)
-    rope_kernel<T, V><<<(unsigned)blocks, threads, 0, st>>>(
-        t1, t2, static_cast<const T*>(cos), static_cast<const T*>(sin), cs_s, sn_s, (int)S,
-        (int)half, rows1, rows_total);
-  else
-    rope_kernel<T, 1><<<(unsigned)blocks, threads, 0, st>>>(
-        t1, t2, static_cast<const T*>(cos), static_cast<const T*>(sin), cs_s, sn_s, (int)S,
-        (int)half, rows1, rows_total);
+  const bool idx32 = blocks * threads < (1LL << 32);
+#define LC_ROPE(VEC_, I_)                                                                 \
+  rope_kernel<T, VEC_, I_><<<(unsigned)blocks, threads, 0, st>>>(                         \
+      t1, t2, static_cast<const T*>(cos), static_cast<const T*>(sin), cs_s, sn_s, (int)S, \
+      (int)half, rows1, rows_total)
+  if (vec_ok) {
+    if (idx32)
+      LC_ROPE(V, uint32_t);
+    else
+      LC_ROPE(V, int64_t);
+  } else {
+    if (idx32)
+      LC_ROPE(1, uint32_t);
+    else
+      LC_ROPE(1, int64_t);
+  }
+#undef LC_ROPE
   return lc_check_launch("lc_rope_fwd");
 }
 
