@@ -474,15 +474,17 @@ __global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) 
 }
 
 // Cross-split merge: one wave per (b, h). Lanes take one split each to form
-// the weights 2^(lse_s - max) in parallel; the weighted sum then walks the
-// splits 8 at a time with independent, unpredicated row loads (each lane owns
-// VPL consecutive floats of head_dim), so its latency is a few round trips.
+// the weights 2^(lse_s - max) in parallel; the weighted sum walks the splits
+// kBatch at a time with independent, unpredicated row loads (each lane owns
+// VPL consecutive floats of head_dim). The first batch of rows does not depend
+// on the max and is loaded together with the split lses, so a merge of up to
+// kBatch splits costs one memory round trip.
 // out = sum_s w_s o_s / sum_s w_s; lse = (max + log2 sum_s w_s) * ln 2.
 template <typename T, int VPL>
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, T* __restrict__ out,
                                                           int64_t o_sb, int64_t o_sh,
                                                           float* __restrict__ lse_out) {
-  constexpr int kBatch = 8;
+  constexpr int kBatch = 16;  // divides 64: a batch never spans two lse chunks
   const int lane = threadIdx.x;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
@@ -492,9 +494,26 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, T* __res
   T* oh = out + (int64_t)b * o_sb + (int64_t)h * o_sh;
   const int d0 = lane * VPL;
   const int dl = d0 < a.D ? d0 : 0;  // lanes past head_dim read (and drop) column 0
+  const float* rows = a.part_o + pbase * a.D + dl;
 
-  float mx = -INFINITY;
-  for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, a.part_lse[pbase + s]);
+  // Rows j0 .. j0 + kBatch - 1, clamped to the last split (nsplit >= 1).
+  float v[kBatch][VPL];
+  auto load_batch = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int jj = 0; jj < kBatch; ++jj) {
+      const int j = min(j0 + jj, nsplit - 1);
+#pragma unroll
+      for (int e = 0; e < VPL; ++e) v[jj][e] = rows[(int64_t)j * a.D + e];
+    }
+  };
+
+  float lse0 = -INFINITY;  // split `lane` of the first 64
+  if (nsplit > 0) {
+    if (lane < nsplit) lse0 = a.part_lse[pbase + lane];
+    load_batch(0);
+  }
+  float mx = lse0;
+  for (int s = lane + 64; s < nsplit; s += 64) mx = fmaxf(mx, a.part_lse[pbase + s]);
   mx = lc_wave_max(mx);
   float acc[VPL];
 #pragma unroll
@@ -503,17 +522,12 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, T* __res
   if (mx != -INFINITY) {
     for (int s0 = 0; s0 < nsplit; s0 += 64) {
       const int n = min(64, nsplit - s0);
-      const float w = lane < n ? lc_exp2(a.part_lse[pbase + s0 + lane] - mx) : 0.f;
+      float ls = lse0;
+      if (s0 > 0) ls = lane < n ? a.part_lse[pbase + s0 + lane] : -INFINITY;
+      const float w = lane < n ? lc_exp2(ls - mx) : 0.f;
       wlane += w;
-      const float* rows = a.part_o + (pbase + s0) * a.D + dl;
       for (int j0 = 0; j0 < n; j0 += kBatch) {
-        float v[kBatch][VPL];
-#pragma unroll
-        for (int jj = 0; jj < kBatch; ++jj) {
-          const int j = min(j0 + jj, n - 1);
-#pragma unroll
-          for (int e = 0; e < VPL; ++e) v[jj][e] = rows[(int64_t)j * a.D + e];
-        }
+        if (s0 + j0 > 0) load_batch(s0 + j0);
 #pragma unroll
         for (int jj = 0; jj < kBatch; ++jj) {
           const float wj = __int_as_float(
