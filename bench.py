@@ -183,6 +183,20 @@ def run_decode(args, shape):
     return result
 
 
+CONFIG3_SHAPE = (4, 32, 8, 4096, 128)  # B, Hq, Hkv, S, D
+
+
+def prefill_shape(args):
+    """(B, Hq, Hkv, S, D) of the prefill workload: config 3 unless --prefill-shape."""
+    text = getattr(args, "prefill_shape", None)
+    if not text:
+        return CONFIG3_SHAPE
+    vals = tuple(int(x) for x in text.split(","))
+    if len(vals) != 5 or min(vals) <= 0 or vals[1] % vals[2] != 0:
+        raise ValueError(f"--prefill-shape wants B,Hq,Hkv,S,D with Hq % Hkv == 0, got {text!r}")
+    return vals
+
+
 def run_prefill(args):
     import torch
 
@@ -190,7 +204,8 @@ def run_prefill(args):
     from llm_cuda.models.llama3.rotary import apply_rotary, build_rope_cache
 
     dev = torch.device("cuda", 0)
-    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    B, Hq, Hkv, S, D = prefill_shape(args)
+    config3 = (B, Hq, Hkv, S, D) == CONFIG3_SHAPE
     g = torch.Generator(device=dev).manual_seed(0)
     q = torch.randn(B, Hq, S, D, generator=g, device=dev, dtype=torch.bfloat16)
     k = torch.randn(B, Hkv, S, D, generator=g, device=dev, dtype=torch.bfloat16)
@@ -212,27 +227,30 @@ def run_prefill(args):
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 5),
         "dtype": "bf16",
-        "config": {"workload": "causal prefill attention, Llama-3-8B shape (BASELINE config 3)",
+        "config": {"workload": ("causal prefill attention, Llama-3-8B shape (BASELINE config 3)"
+                                if config3 else "causal prefill attention, shape from --prefill-shape"),
                    "batch": B, "seq_len": S, "n_q_heads": Hq, "n_kv_heads": Hkv, "head_dim": D,
                    "rope_theta": 500000.0, "flops_per_step": flops},
         "roofline": {"bound": "mfma", "kernel": "prefill attention", "achieved": round(tflops, 2),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic("prefill_attn_8b")},
+                     # the committed counter summary covers the config-3 shape only
+                     "traffic": measured_traffic("prefill_attn_8b") if config3 else None},
     }
     if not args.no_cpu_baseline:
         from oracle.attention import causal_attention
 
         torch.set_num_threads(cpu_threads())
-        # one batch element, one kv-head group (4 q heads) = 1/32 of the work
-        qs, ks, vs = q[:1, :4].cpu(), k[:1, :1].cpu(), v[:1, :1].cpu()
+        # one batch element, one kv-head group (G q heads): 1 / (B * Hkv) of the work
+        G = Hq // Hkv
+        qs, ks, vs = q[:1, :G].cpu(), k[:1, :1].cpu(), v[:1, :1].cpu()
         secs = timed_cpu(lambda: causal_attention(qs, ks, vs), budget_s=40.0)
-        sflops = 2 * 1 * 4 * D * S * (S + 1)
+        sflops = 2 * 1 * G * D * S * (S + 1)
         result["cpu_baseline"] = {
             "value": round(sflops / secs / 1e12, 4), "unit": "TFLOP/s",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"batch 0, q heads 0-3 / kv head 0 (1/32 of the step), torch fp32 "
-                      f"oracle.attention.causal_attention: {secs:.3f} s"}
+            "sample": f"batch 0, q heads 0-{G - 1} / kv head 0 (1/{B * Hkv} of the step), torch "
+                      f"fp32 oracle.attention.causal_attention: {secs:.3f} s"}
     return result
 
 
@@ -673,6 +691,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gemm-tuning", dest="tune_gemms", action="store_false",
                         help="model8b: keep torch's default GEMM solutions (no TunableOp)")
+    parser.add_argument("--prefill-shape", default=None, metavar="B,Hq,Hkv,S,D",
+                        help="prefill: another shape instead of config 3 (4,32,8,4096,128)")
     parser.add_argument("--no-secondary", dest="secondary", action="store_false",
                         help="decode8b: skip the prefill (config 3) and decode-step (config 4) "
                              "figures added to the line under 'secondary'")
@@ -739,6 +759,7 @@ def run_secondary(args) -> dict:
 
     sub = copy.copy(args)
     sub.no_cpu_baseline = True
+    sub.prefill_shape = None  # the secondary prefill figure is config 3
     out = {}
     for key, fn in (("prefill_config3", run_prefill), ("decode_step_config4", run_model)):
         try:
