@@ -343,10 +343,10 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
 }
 
 // Page sizes that are not multiples of 32: per-lane page resolution.
-template <typename T, int DPAD>
 // Three waves per SIMD up to head_dim 128: at 144 VGPRs and 9 KiB of LDS the
 // kernel fits them without spills, and the extra loads in flight measured 6%
 // faster than two. (head_dim 256 would spill at three.)
+template <typename T, int DPAD>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(DPAD <= 128 ? 3 : 1))) void
 paged_decode_lanes_kernel(DecodeArgs a) {
   typedef MfmaOps<T> Ops;
