@@ -21,6 +21,7 @@
 //     partials to the final id (int64) and, optionally, the winning logit.
 // HBM-bound: the weight (V x K x 2 bytes, 1.05 GB for Llama-3-8B) is read once.
 #include <limits.h>
+#include <algorithm>
 #include <math.h>
 
 #include <type_traits>
@@ -125,7 +126,11 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
     for (int u = 0; u < NIW_H; ++u) {
       const int row = (wave * NIW_H + u) * RPI + lane / CPR;
       const int ch = (lane % CPR) ^ pf_swz<CPR>(row);
-      o.o[u] = static_cast<int>(((int64_t)row * a.hs + ch * 8) * sizeof(T));
+      // Rows past B get an offset of 2^31 bytes: beyond the descriptor's
+      // range (< 2^31) with any tile offset added, so they load zeros, and
+      // their row * stride is never formed (it may not fit 32 bits).
+      o.o[u] = row < a.B ? static_cast<int>(((int64_t)row * a.hs + ch * 8) * sizeof(T))
+                         : INT_MIN;
     }
     return o;
   }();
@@ -368,7 +373,8 @@ int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void*
                     lc_aligned(hidden, 16) && lc_aligned(weight, 16) &&
                     hidden_row_stride % 8 == 0 && weight_row_stride % 8 == 0 &&
                     ((int64_t)kLhRows * weight_row_stride) * esz < (1LL << 31) &&
-                    ((int64_t)kLhBatch * hidden_row_stride) * esz < (1LL << 31);
+                    ((int64_t)(std::min<int64_t>(B, kLhBatch) - 1) * hidden_row_stride + K) *
+                            esz < (1LL << 31);
   hipStream_t st = lc_stream(stream);
   switch (dtype) {
     case LC_DTYPE_F32:

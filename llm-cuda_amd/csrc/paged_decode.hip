@@ -689,8 +689,9 @@ int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                     lc_aligned(value_pages, 16);
   // Row kernel: every 32-token step stays inside one page, a split touches at
   // most 64 pages (one per lane), and a page's head slice is addressable with
-  // 31-bit byte offsets.
-  const bool rows = page_size % 32 == 0 && split_tokens / page_size + 1 <= 64 &&
+  // 31-bit byte offsets. A split that does not start on a page boundary
+  // touches up to (split_tokens - 1) / page_size + 2 pages.
+  const bool rows = page_size % 32 == 0 && (split_tokens - 1) / page_size + 2 <= 64 &&
                     ((page_size - 1) * kv_s_tok + D) * esz < (1LL << 31);
   hipStream_t st = lc_stream(stream);
   switch (dtype) {

@@ -46,9 +46,41 @@ class _DeviceGuard:
 
 
 # ---------------------------------------------------------------------------
+# Forward-only kernels under autograd
+# ---------------------------------------------------------------------------
+class _ForwardOnly(torch.autograd.Function):
+    """Runs a forward-only kernel inside the autograd graph so that a backward
+    pass through its outputs raises instead of silently skipping every input
+    upstream of it (the kernel has no backward in this build)."""
+
+    @staticmethod
+    def forward(ctx, name, fn, *inputs):
+        ctx.name = name
+        return fn(*inputs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(
+            f"{ctx.name} has no backward in this build (inference path only); run the "
+            "forward under torch.no_grad() or with inputs that do not require grad")
+
+
+def _records_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in tensors)
+
+
+# ---------------------------------------------------------------------------
 # RMSNorm  (reference: kernels/triton/rmsnorm.py:46-75, norm.py:22-33)
 # ---------------------------------------------------------------------------
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """y = x * rsqrt(mean(x^2) + eps) * weight over the last dimension (forward only)."""
+    if _records_grad(x, weight):
+        return _ForwardOnly.apply("rms_norm", lambda a, w: _rms_norm(a, w, eps), x, weight)
+    return _rms_norm(x, weight, eps)
+
+
+def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     dev = nat.require_device(x, weight)
     if weight.dim() != 1 or weight.shape[0] != x.shape[-1]:
         raise ValueError(f"weight shape {tuple(weight.shape)} does not match hidden {x.shape[-1]}")
@@ -75,7 +107,20 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, 
 
     One pass over the rows instead of an add and a norm (reference pair:
     models/llama3/model.py:29-42). With inplace=True, s is written into x.
+    Forward only: a backward through y or s raises.
     """
+    if _records_grad(x, residual, weight):
+        if inplace:
+            raise NotImplementedError(
+                "in-place add_rms_norm cannot be recorded by autograd (forward-only kernel)")
+        return _ForwardOnly.apply(
+            "add_rms_norm", lambda a, r, w: _add_rms_norm(a, r, w, eps, False), x, residual,
+            weight)
+    return _add_rms_norm(x, residual, weight, eps, inplace)
+
+
+def _add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+                  inplace: bool):
     dev = nat.require_device(x, residual, weight)
     if x.shape != residual.shape or x.dtype != residual.dtype:
         raise ValueError("x and residual must have the same shape and dtype")
@@ -109,6 +154,13 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, 
 # SwiGLU  (reference: kernels/triton/swiglu.py:91-145,199-200)
 # ---------------------------------------------------------------------------
 def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up in fp32, rounded to gate's dtype (forward only)."""
+    if _records_grad(gate, up):
+        return _ForwardOnly.apply("swiglu", _swiglu, gate, up)
+    return _swiglu(gate, up)
+
+
+def _swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     if gate.shape != up.shape:
         raise ValueError("gate and up must have matching shapes")
     if gate.dtype != up.dtype:
@@ -151,7 +203,17 @@ def _check_rope_operand(x: torch.Tensor, cos: torch.Tensor, name: str) -> None:
 
 def rope(x1: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
          x2: torch.Tensor | None = None):
-    """Rotate x1 (and x2) in one launch; returns contiguous new tensors."""
+    """Rotate x1 (and x2) in one launch; returns contiguous new tensors (forward only)."""
+    if _records_grad(x1, x2, cos, sin):
+        if x2 is None:
+            return _ForwardOnly.apply("rope", lambda a, c, s_: _rope(a, c, s_, None)[0], x1,
+                                      cos, sin), None
+        return _ForwardOnly.apply("rope", _rope, x1, cos, sin, x2)
+    return _rope(x1, cos, sin, x2)
+
+
+def _rope(x1: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+          x2: torch.Tensor | None = None):
     if cos.shape != sin.shape or cos.dtype != sin.dtype:
         raise ValueError("cos and sin must have the same shape and dtype")
     _check_rope_operand(x1, cos, "x")
@@ -288,10 +350,11 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
     hidden = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
     weight = weight if weight.stride(-1) == 1 else weight.contiguous()
     B, K = hidden.shape
-    # The MFMA path addresses up to 32 hidden rows with 32-bit byte offsets; a
-    # widely strided view (the last position of a long prompt) is packed first
-    # (B x K elements) rather than sent to the generic kernel.
-    if B > 1 and min(B, 32) * hidden.stride(0) * hidden.element_size() >= 2 ** 31:
+    # The MFMA path addresses the hidden rows of one 32-row chunk with 32-bit
+    # byte offsets (the library's own condition); a widely strided view (the
+    # last position of a long prompt) is packed first (B x K elements) rather
+    # than sent to the generic kernel.
+    if B > 1 and ((min(B, 32) - 1) * hidden.stride(0) + K) * hidden.element_size() >= 2 ** 31:
         hidden = hidden.contiguous()
     V = weight.shape[0]
     ids = torch.empty(B, dtype=torch.int64, device=dev)
@@ -331,12 +394,22 @@ def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Te
                  block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None = None,
                  return_lse: bool = False, split_tokens: int | None = None,
                  workspace: torch.Tensor | None = None):
-    """One-token GQA attention per sequence over a paged K/V pool.
+    """One-token GQA attention per sequence over a paged K/V pool (forward only).
 
     q: [B, Hq, 1, D] or [B, Hq, D]; key_pages, value_pages: [N, Hkv, P, D];
     block_table: int32 [B, max_pages]; seq_lens: int32 [B]. Returns out with
     q's shape (and lse [B, Hq] fp32 if return_lse).
     """
+    args = (block_table, seq_lens, scale, return_lse, split_tokens, workspace)
+    if _records_grad(q, key_pages, value_pages):
+        return _ForwardOnly.apply("paged_decode", lambda a, k, v: _paged_decode(a, k, v, *args),
+                                  q, key_pages, value_pages)
+    return _paged_decode(q, key_pages, value_pages, *args)
+
+
+def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
+                  block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None,
+                  return_lse: bool, split_tokens: int | None, workspace: torch.Tensor | None):
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
     if q4.dim() != 4 or q4.shape[2] != 1:
@@ -450,8 +523,17 @@ def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch
     Rotates q and k at positions seq_lens[b] + s (cos/sin: full tables indexed
     by position, covering the block-table capacity), writes the rotated k and
     v into the page pools, advances seq_lens by S in place and returns the
-    rotated q as a new contiguous [B, Hq, S, D] tensor.
+    rotated q as a new contiguous [B, Hq, S, D] tensor. Forward only.
     """
+    if _records_grad(q, k, v):
+        return _ForwardOnly.apply(
+            "rope_kv_append",
+            lambda a, b, c: _rope_kv_append(a, b, c, cos, sin, key_pages, value_pages,
+                                            block_table, seq_lens), q, k, v)
+    return _rope_kv_append(q, k, v, cos, sin, key_pages, value_pages, block_table, seq_lens)
+
+
+def _rope_kv_append(q, k, v, cos, sin, key_pages, value_pages, block_table, seq_lens):
     _pool_checks(key_pages, value_pages, block_table)
     if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
         raise ValueError("q must be [B, Hq, S, D] and k, v [B, Hkv, S, D]")

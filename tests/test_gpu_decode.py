@@ -230,3 +230,30 @@ def test_paged_lengths_outside_the_table_are_clamped(cuda, dtype):
     out, lse = _run_paged(q, kp, vp, bt, torch.tensor([-7, 64, 0], dtype=torch.int32), cuda)
     assert (out[0].float().cpu() == 0).all() and torch.isinf(lse[0].cpu()).all()
     assert (out[2].float().cpu() == 0).all() and torch.isinf(lse[2].cpu()).all()
+
+
+def test_unaligned_split_touching_65_pages(cuda):
+    """Page size 160 with 10176-token splits: the second split starts 96 tokens
+    into a page and touches 65 pages, one more than the row kernel's
+    one-page-per-lane table holds; such a launch must take a kernel that
+    resolves every page (the first split touches 64)."""
+    lens = [20500, 10300]
+    q, kp, vp, bt, sl = _paged_case(lens, 8, 2, 128, 160, torch.bfloat16, cuda, seed=31)
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda, split_tokens=10176)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert_close(out, ref, ATOL[torch.bfloat16], "65-page split")
+    assert_lse_close(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 48])
+@pytest.mark.parametrize("P", [16, 48])
+def test_paged_lanes_kernel_small_head_dim(cuda, dtype, D, P):
+    """Page sizes that are not multiples of 32 run the per-lane-page kernel; at
+    head_dim <= 64 it is the 64-wide instance (48 is padded to 64)."""
+    lens = [1, 17, 96, 200, 511, 47]
+    q, kp, vp, bt, sl = _paged_case(lens, 16, 4, D, P, dtype, cuda, seed=D + P)
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert_close(out, ref, ATOL[dtype], f"lanes D={D} P={P}")
+    assert_lse_close(lse, ref_lse)
