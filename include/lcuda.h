@@ -4,7 +4,8 @@
  *
  * Conventions shared by every entry point:
  *   - Pointers are device pointers owned by the caller. The library never
- *     allocates or frees device memory and keeps no device state.
+ *     allocates or frees device memory and keeps no device state, except the
+ *     fixed scratch array behind lc_paged_decode_fwd_noalloc.
  *   - Sizes and strides are int64 counts of ELEMENTS (not bytes). The last
  *     (head_dim / hidden) dimension must have stride 1.
  *   - `dtype` is one of LC_DTYPE_*; all inputs and outputs of one call share it
@@ -44,7 +45,7 @@ enum {
   LC_OK = 0,
   LC_EINVAL = -1,       /* bad argument (shape, stride, dtype, null pointer) */
   LC_EUNSUPPORTED = -2, /* valid request this build does not implement       */
-  LC_EWORKSPACE = -3,   /* caller-provided workspace too small               */
+  LC_EWORKSPACE = -3,   /* workspace (or the fixed scratch) too small        */
 };
 
 /* Library identity. Replaces the extension self-check of
@@ -193,6 +194,35 @@ LC_API int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const 
                         int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                         int64_t page_size, int64_t split_tokens, int64_t max_splits, float scale,
                         int dtype, void* stream);
+
+/* Size of the device scratch behind lc_paged_decode_fwd_noalloc: the largest
+ * lc_paged_decode_workspace_bytes(B, Hq, D, max_splits) it accepts (32 MiB:
+ * e.g. B 64 x 32 heads x 16 splits x head_dim 128 at the 8B shape, or
+ * B 8 x 64 heads x 64 splits x 128 at the 70B long-context shape). */
+#define LC_DECODE_NOALLOC_SCRATCH_BYTES (32LL << 20)
+
+/* lc_paged_decode_fwd without a workspace argument: the split partials live in
+ * a fixed device array of LC_DECODE_NOALLOC_SCRATCH_BYTES owned by the library
+ * (one per GPU, held until the process ends). No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc). It allocates
+ * nothing and calls no allocating routine; the first call on a device looks
+ * up that device's copy of the array once. Semantics and arguments are those
+ * of lc_paged_decode_fwd; the stream must belong to the current device.
+ * Returns LC_EWORKSPACE (no launch) when the partials of (B, Hq, D,
+ * max_splits) exceed the scratch. Every call on one GPU shares its scratch:
+ * calls that overlap on that GPU (other streams or threads) race and must be
+ * serialised by the caller. Nothing in the scratch needs to start at zero. */
+LC_API int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                                       const void* key_pages, const void* value_pages,
+                                       int64_t kv_s_page, int64_t kv_s_head, int64_t kv_s_tok,
+                                       const int32_t* block_table, int64_t bt_stride,
+                                       int64_t max_pages_per_seq, int64_t num_pages,
+                                       const int32_t* seq_lens, void* out, int64_t o_sb,
+                                       int64_t o_sh, float* lse, int64_t B, int64_t Hq,
+                                       int64_t Hkv, int64_t D, int64_t page_size,
+                                       int64_t split_tokens, int64_t max_splits, float scale,
+                                       int dtype, void* stream);
 
 /* Scatter S new tokens per sequence into the page pools through the block
  * table: pages[bt[b, (p0_b+s)/P], h, (p0_b+s)%P, :] = x[b, h, s, :] with

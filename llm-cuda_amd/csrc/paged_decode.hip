@@ -25,6 +25,8 @@
 // kernel combines splits with weights 2^(lse_s - lse).
 #include <math.h>
 
+#include <mutex>
+
 #include "lc_common.h"
 
 namespace {
@@ -603,52 +605,39 @@ int launch_decode(DecodeArgs a, void* out, int64_t o_sb, int64_t o_sh, float* ls
   return launch_merge<T>(a, out, o_sb, o_sh, lse, st);
 }
 
-}  // namespace
-
-extern "C" {
-
-int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits) {
-  if (B < 0 || Hq < 0 || D < 0 || max_splits < 0) return -1;
-  const int64_t n = B * Hq * max_splits;
-  // partial o (fp32, D per split), then partial lse (fp32), 256-byte aligned.
-  const int64_t o_bytes = ((n * D * 4) + 255) / 256 * 256;
-  return o_bytes + n * 4;
-}
-
-int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* key_pages,
-                        const void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
-                        int64_t kv_s_tok, const int32_t* block_table, int64_t bt_stride,
-                        int64_t max_pages_per_seq, int64_t num_pages, const int32_t* seq_lens,
-                        void* out, int64_t o_sb, int64_t o_sh, float* lse, void* workspace,
-                        int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
-                        int64_t page_size, int64_t split_tokens, int64_t max_splits, float scale,
-                        int dtype, void* stream) {
+// Validates a decode call and launches it with the given workspace (the
+// caller's, or the device scratch of the allocation-free entry point).
+int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh,
+                      const void* key_pages, const void* value_pages, int64_t kv_s_page,
+                      int64_t kv_s_head, int64_t kv_s_tok, const int32_t* block_table,
+                      int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
+                      const int32_t* seq_lens, void* out, int64_t o_sb, int64_t o_sh, float* lse,
+                      void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
+                      int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
+                      int64_t max_splits, float scale, int dtype, void* stream) {
   LC_REQUIRE((q && key_pages && value_pages && block_table && seq_lens && out && workspace) ||
                  B == 0,
-             "lc_paged_decode_fwd: null pointer");
-  LC_REQUIRE(B >= 0 && B < 65536, "lc_paged_decode_fwd: batch %lld out of range", (long long)B);
+             "%s: null pointer", who);
+  LC_REQUIRE(B >= 0 && B < 65536, "%s: batch %lld out of range", who, (long long)B);
   LC_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
-             "lc_paged_decode_fwd: n_heads (%lld) must be a multiple of n_kv_heads (%lld)",
-             (long long)Hq, (long long)Hkv);
-  LC_REQUIRE(D > 0 && D <= 256, "lc_paged_decode_fwd: head_dim %lld not in [1, 256]",
-             (long long)D);
+             "%s: n_heads (%lld) must be a multiple of n_kv_heads (%lld)", who, (long long)Hq,
+             (long long)Hkv);
+  LC_REQUIRE(D > 0 && D <= 256, "%s: head_dim %lld not in [1, 256]", who, (long long)D);
   LC_REQUIRE(page_size > 0 && max_pages_per_seq > 0 && num_pages > 0,
-             "lc_paged_decode_fwd: page_size, max_pages_per_seq and num_pages must be > 0");
+             "%s: page_size, max_pages_per_seq and num_pages must be > 0", who);
   LC_REQUIRE(max_pages_per_seq * page_size < (1LL << 31) && num_pages < (1LL << 31),
-             "lc_paged_decode_fwd: cache too large for 32-bit token indices");
-  LC_REQUIRE(bt_stride >= max_pages_per_seq, "lc_paged_decode_fwd: bt_stride < row length");
+             "%s: cache too large for 32-bit token indices", who);
+  LC_REQUIRE(bt_stride >= max_pages_per_seq, "%s: bt_stride < row length", who);
   LC_REQUIRE(split_tokens > 0 && split_tokens % 64 == 0,
-             "lc_paged_decode_fwd: split_tokens must be a positive multiple of 64");
-  LC_REQUIRE(max_splits <= 65535, "lc_paged_decode_fwd: max_splits %lld > 65535",
-             (long long)max_splits);
+             "%s: split_tokens must be a positive multiple of 64", who);
+  LC_REQUIRE(max_splits <= 65535, "%s: max_splits %lld > 65535", who, (long long)max_splits);
   LC_REQUIRE(max_splits > 0 && max_splits * split_tokens >= max_pages_per_seq * page_size,
-             "lc_paged_decode_fwd: max_splits * split_tokens must cover the block-table "
-             "capacity (%lld tokens)",
-             (long long)(max_pages_per_seq * page_size));
+             "%s: max_splits * split_tokens must cover the block-table capacity (%lld tokens)",
+             who, (long long)(max_pages_per_seq * page_size));
   const int64_t need = lc_paged_decode_workspace_bytes(B, Hq, D, max_splits);
-  LC_REQUIRE(workspace_bytes >= need, "lc_paged_decode_fwd: workspace %lld < %lld bytes",
+  LC_REQUIRE(workspace_bytes >= need, "%s: workspace %lld < %lld bytes", who,
              (long long)workspace_bytes, (long long)need);
-  LC_REQUIRE(lc_aligned(workspace, 256), "lc_paged_decode_fwd: workspace not 256-byte aligned");
+  LC_REQUIRE(lc_aligned(workspace, 256), "%s: workspace not 256-byte aligned", who);
   if (B == 0) return LC_OK;
 
   DecodeArgs a{};
@@ -702,8 +691,114 @@ int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* k
     case LC_DTYPE_F16:
       return launch_decode<f16_t>(a, out, o_sb, o_sh, lse, mfma, rows, st);
     default:
-      return lc_fail(LC_EINVAL, "lc_paged_decode_fwd: unknown dtype %d", dtype);
+      return lc_fail(LC_EINVAL, "%s: unknown dtype %d", who, dtype);
   }
+}
+
+// Device scratch of lc_paged_decode_fwd_noalloc, one per device (its address
+// differs per device). Host code uses the address kept in g_scratch_ptr, never
+// the symbol itself (on the host the name is only a handle).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once per device; the
+// stream must belong to the current device.
+int scratch_for_stream(const char* who, void* stream, void** out);
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[LC_DECODE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+int scratch_for_stream(const char* who, void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return lc_fail(static_cast<int>(e), "%s: hipGetDevice failed: %s", who,
+                                      hipGetErrorString(e));
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(lc_stream(stream), &sdev);
+    if (e != hipSuccess)
+      return lc_fail(static_cast<int>(e), "%s: hipStreamGetDevice failed: %s", who,
+                     hipGetErrorString(e));
+    if (sdev != dev)
+      return lc_fail(LC_EINVAL, "%s: the stream belongs to device %d, the current device is %d",
+                     who, sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices)
+    return lc_fail(LC_EUNSUPPORTED, "%s: device %d beyond the %d this library tracks", who, dev,
+                   kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return lc_fail(e != hipSuccess ? static_cast<int>(e) : LC_EUNSUPPORTED,
+                     "%s: no address for the device scratch on device %d: %s", who, dev,
+                     hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits) {
+  if (B < 0 || Hq < 0 || D < 0 || max_splits < 0) return -1;
+  const int64_t n = B * Hq * max_splits;
+  // partial o (fp32, D per split), then partial lse (fp32), 256-byte aligned.
+  const int64_t o_bytes = ((n * D * 4) + 255) / 256 * 256;
+  return o_bytes + n * 4;
+}
+
+int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* key_pages,
+                        const void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
+                        int64_t kv_s_tok, const int32_t* block_table, int64_t bt_stride,
+                        int64_t max_pages_per_seq, int64_t num_pages, const int32_t* seq_lens,
+                        void* out, int64_t o_sb, int64_t o_sh, float* lse, void* workspace,
+                        int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                        int64_t page_size, int64_t split_tokens, int64_t max_splits, float scale,
+                        int dtype, void* stream) {
+  return paged_decode_impl("lc_paged_decode_fwd", q, q_sb, q_sh, key_pages, value_pages,
+                           kv_s_page, kv_s_head, kv_s_tok, block_table, bt_stride,
+                           max_pages_per_seq, num_pages, seq_lens, out, o_sb, o_sh, lse,
+                           workspace, workspace_bytes, B, Hq, Hkv, D, page_size, split_tokens,
+                           max_splits, scale, dtype, stream);
+}
+
+int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                                const void* key_pages, const void* value_pages,
+                                int64_t kv_s_page, int64_t kv_s_head, int64_t kv_s_tok,
+                                const int32_t* block_table, int64_t bt_stride,
+                                int64_t max_pages_per_seq, int64_t num_pages,
+                                const int32_t* seq_lens, void* out, int64_t o_sb, int64_t o_sh,
+                                float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                int64_t page_size, int64_t split_tokens, int64_t max_splits,
+                                float scale, int dtype, void* stream) {
+  static const char* who = "lc_paged_decode_fwd_noalloc";
+  if (B == 0) return LC_OK;
+  const int64_t need = lc_paged_decode_workspace_bytes(B, Hq, D, max_splits);
+  if (need > LC_DECODE_NOALLOC_SCRATCH_BYTES)
+    return lc_fail(LC_EWORKSPACE,
+                   "%s: %lld bytes of split partials (batch %lld x %lld heads x %lld splits x "
+                   "head_dim %lld) exceed the %lld-byte device scratch; use fewer or larger "
+                   "splits, or lc_paged_decode_fwd with a workspace",
+                   who, (long long)need, (long long)B, (long long)Hq, (long long)max_splits,
+                   (long long)D, (long long)LC_DECODE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_for_stream(who, stream, &ws);
+  if (rc != LC_OK) return rc;
+  // No part of the scratch needs clearing: every split with tokens writes its
+  // partials, and the merge reads only those splits.
+  return paged_decode_impl(who, q, q_sb, q_sh, key_pages, value_pages, kv_s_page, kv_s_head,
+                           kv_s_tok, block_table, bt_stride, max_pages_per_seq, num_pages,
+                           seq_lens, out, o_sb, o_sh, lse, ws, LC_DECODE_NOALLOC_SCRATCH_BYTES, B,
+                           Hq, Hkv, D, page_size, split_tokens, max_splits, scale, dtype, stream);
 }
 
 }  // extern "C"

@@ -78,6 +78,12 @@ _SIGNATURES = {
          _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
     ),
+    "lc_paged_decode_fwd_noalloc": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
+         _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
+    ),
     "lc_paged_kv_append": (
         ctypes.c_int,
         [_c_p, _c_p, _c_i64p, _c_i64p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64,
