@@ -98,20 +98,31 @@ LC_API int lc_rope_fwd(const void* x1, void* out1, int64_t h1, const int64_t* x1
                 const void* sin, int64_t cos_stride_s, int64_t sin_stride_s, int64_t B,
                 int64_t S, int64_t D, int dtype, void* stream);
 
-/* Causal attention forward with native GQA and logsumexp.
- * o[b,h,i,:] = sum_j softmax_j(q[b,h,i,:].k[b,h/G,j,:] * scale) v[b,h/G,j,:]
+/* Causal attention forward with native GQA, an optional additive mask and
+ * logsumexp.
+ * o[b,h,i,:] = sum_j softmax_j(q[b,h,i,:].k[b,h/G,j,:] * scale + bias[b,h,i,j])
+ *              v[b,h/G,j,:]
  * over keys j <= i + q_offset (j < Skv); lse[b,h,i] = natural-log logsumexp of
  * the scaled, masked scores (fp32, contiguous [B, Hq, Sq]; may be NULL).
- * Replaces kernels/triton/attention.py:74-178,323-378,501-535 (forward),
+ * Replaces kernels/triton/attention.py:74-178,323-378,501-535 (forward, with
+ * the attention_mask of _torch_sdpa_fallback :457-477),
  * csrc/attention_kernel.cu:12-153 and, for q_offset > 0,
- * models/llama3/attention.py:63-89 (_torch_attention with past_len).
+ * models/llama3/attention.py:63-89 (_torch_attention with past_len and
+ * attention_mask).
  * q, o: [B, Hq, Sq, D]; k, v: [B, Hkv, Skv, D]; strides in *_strides[4].
+ * bias (may be NULL): the additive mask [B, Hq, Sq, Skv] read with element
+ * strides bias_strides[4] (0 broadcasts a dimension), of dtype bias_dtype
+ * (fp32 or the dtype of q). Entries below -1e30 (and NaN) act as -1e30, so a
+ * row whose visible keys are all so masked averages them, as the reference's
+ * softmax of equal scores does; -inf excludes a key, and a row without any
+ * visible key gives o = 0, lse = -inf (the reference gives NaN there).
  * Hq % Hkv == 0. bf16/f16 run on MFMA (D in {64, 128}); other cases run a
  * generic fp32-FMA kernel (D <= 256). */
 LC_API int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D,
                         const int64_t* q_strides, const int64_t* k_strides,
                         const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
+                        const void* bias, const int64_t* bias_strides, int bias_dtype,
                         float scale, int dtype, void* stream);
 
 /* Bytes of workspace lc_prefill_attn_bwd needs: two fp32 values per query row
@@ -123,9 +134,11 @@ LC_API int64_t lc_prefill_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_
  *   dq[b,h,i]   = scale * sum_j dS_ij k[b,h/G,j]
  *   dk[b,g,j]   = scale * sum_{h in group g, i} dS_ij q[b,h,i]
  *   dv[b,g,j]   =         sum_{h in group g, i} P_ij dout[b,h,i]
- * with P_ij = exp(q_i.k_j * scale - lse_i) on keys j <= i + q_offset and
- * dS_ij = P_ij (dout_i.v_j - rowsum(dout_i * o_i)). dq, dk, dv are written,
- * not accumulated (no atomics; no zero-fill needed).
+ * with P_ij = exp(q_i.k_j * scale + bias_ij - lse_i) on keys j <= i + q_offset
+ * and dS_ij = P_ij (dout_i.v_j - rowsum(dout_i * o_i)). dq, dk, dv are
+ * written, not accumulated (no atomics; no zero-fill needed). bias,
+ * bias_strides, bias_dtype: the forward's additive mask (may be NULL); it
+ * gets no gradient.
  * Replaces kernels/triton/attention.py:181-320 (_fused_causal_attn_bwd) and
  * :380-454 (_FusedCausalAttentionFunction.backward), which was MHA-only.
  * q, o, dout, dq: [B, Hq, Sq, D]; k, v, dk, dv: [B, Hkv, Skv, D]; lse fp32
@@ -140,6 +153,7 @@ LC_API int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, cons
                         const int64_t* v_strides, const int64_t* o_strides,
                         const int64_t* do_strides, const int64_t* dq_strides,
                         const int64_t* dk_strides, const int64_t* dv_strides, int64_t q_offset,
+                        const void* bias, const int64_t* bias_strides, int bias_dtype,
                         float scale, void* workspace, int64_t workspace_bytes, int dtype,
                         void* stream);
 
@@ -173,6 +187,12 @@ LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D,
  * slot t % page_size. lse[b,h] (fp32, contiguous [B, Hq], may be NULL) is the
  * natural-log logsumexp of the scaled scores; empty sequences give out = 0,
  * lse = -inf.
+ * bias (may be NULL): an additive mask added to the scaled score of token t
+ * of sequence b for query head h, bias[b*bias_sb + h*bias_sh + t] (strides in
+ * elements, 0 broadcasts) for t < bias_len; tokens at or past bias_len get
+ * none. bias_dtype: LC_DTYPE_F32, _F16 or _BF16. Clamping of very negative
+ * values and -inf as in lc_prefill_attn_fwd (the reference's decode step with
+ * an attention_mask, models/llama3/attention.py:63-89,138-147).
  * Replaces kernels/triton/decode_attention.py:47-159,204-287 reading the
  * contiguous copy made by models/llama3/kv_cache.py:65-83 (get_kv): here the
  * pages are read in place.
@@ -190,10 +210,11 @@ LC_API int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const 
                         const void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
                         int64_t kv_s_tok, const int32_t* block_table, int64_t bt_stride,
                         int64_t max_pages_per_seq, int64_t num_pages, const int32_t* seq_lens,
-                        void* out, int64_t o_sb, int64_t o_sh, float* lse, void* workspace,
-                        int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
-                        int64_t page_size, int64_t split_tokens, int64_t max_splits, float scale,
-                        int dtype, void* stream);
+                        void* out, int64_t o_sb, int64_t o_sh, float* lse, const void* bias,
+                        int64_t bias_sb, int64_t bias_sh, int64_t bias_len, int bias_dtype,
+                        void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
+                        int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
+                        int64_t max_splits, float scale, int dtype, void* stream);
 
 /* Size of the device scratch behind lc_paged_decode_fwd_noalloc: the largest
  * lc_paged_decode_workspace_bytes(B, Hq, D, max_splits) it accepts (32 MiB:
@@ -219,10 +240,11 @@ LC_API int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh
                                        const int32_t* block_table, int64_t bt_stride,
                                        int64_t max_pages_per_seq, int64_t num_pages,
                                        const int32_t* seq_lens, void* out, int64_t o_sb,
-                                       int64_t o_sh, float* lse, int64_t B, int64_t Hq,
-                                       int64_t Hkv, int64_t D, int64_t page_size,
-                                       int64_t split_tokens, int64_t max_splits, float scale,
-                                       int dtype, void* stream);
+                                       int64_t o_sh, float* lse, const void* bias,
+                                       int64_t bias_sb, int64_t bias_sh, int64_t bias_len,
+                                       int bias_dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                       int64_t D, int64_t page_size, int64_t split_tokens,
+                                       int64_t max_splits, float scale, int dtype, void* stream);
 
 /* Scatter S new tokens per sequence into the page pools through the block
  * table: pages[bt[b, (p0_b+s)/P], h, (p0_b+s)%P, :] = x[b, h, s, :] with

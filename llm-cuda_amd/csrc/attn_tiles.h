@@ -4,6 +4,8 @@
 // pipeline stages.
 #pragma once
 
+#include <type_traits>
+
 #include "lc_common.h"
 
 namespace lc_attn {
@@ -87,6 +89,68 @@ __device__ __forceinline__ void pf_dma_tile(const void* base, int nbytes, LC_LDS
                                              0, AUX);
   }
 }
+
+// Additive bias of one 64-key tile for the query row of each lane, in the
+// layout of the 32x32 S^T accumulators: lane (l32 = query row, hh = lane / 32)
+// holds keys k0 + kt*32 + j*8 + hh*4 + e (kt < 2, j < 4, e < 4), i.e. register
+// kt, 4j + e. Storage: BIAS 1 = the data type T (bf16/f16), 2 = fp32. Loads go
+// through a buffer descriptor over the row's (b, head) slice, so keys and rows
+// past its end read 0 (those scores are masked or discarded anyway).
+template <typename T, int BIAS>
+struct BiasTile {
+  static constexpr int ESZ = BIAS == 2 ? 4 : 2;
+  typedef u32x4_t r4_t;
+  typedef u32x2_t r2_t;
+  typedef typename std::conditional<BIAS == 2, r4_t, r2_t>::type raw_t;
+  raw_t r[2][4];
+
+  // row_b: byte offset of the lane's query row in the slice; s3_b: key stride
+  // in bytes; vec: keys contiguous and every 4-key group 4*ESZ-aligned and
+  // wholly inside or outside the slice (one 8- or 16-byte load per group).
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int row_b, int k0, int hh,
+                                       int s3_b, bool vec) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = k0 + kt * 32 + j * 8 + hh * 4;
+        if (vec) {
+          const int off = row_b + key * ESZ;
+          if constexpr (BIAS == 2)
+            r[kt][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+          else
+            r[kt][j] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int off = row_b + (key + e) * s3_b;
+            if constexpr (BIAS == 2) {
+              r[kt][j][e] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+            } else {
+              const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+              if (e & 1)
+                r[kt][j][e >> 1] |= h << 16;
+              else
+                r[kt][j][e >> 1] = h;
+            }
+          }
+        }
+      }
+  }
+  // Element (kt, 4j + e) in the exp2 domain (lc_bias_log2).
+  __device__ __forceinline__ float log2_at(int kt, int r4) const {
+    const int j = r4 >> 2, e = r4 & 3;
+    float x;
+    if constexpr (BIAS == 2) {
+      x = __uint_as_float(r[kt][j][e]);
+    } else {
+      const uint32_t w = r[kt][j][e >> 1];
+      const uint16_t h = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+      x = static_cast<float>(__builtin_bit_cast(T, h));
+    }
+    return lc_bias_log2(x);
+  }
+};
 
 // Maximum of x over the two 32-lane halves of the wave (v_permlane32_swap).
 __device__ __forceinline__ float pf_half_max(float x) {

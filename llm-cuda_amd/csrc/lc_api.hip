@@ -28,7 +28,7 @@ int lc_check_launch(const char* what) {
 extern "C" {
 
 // Major * 10000 + minor * 100 + patch.
-int lc_version(void) { return 100; }
+int lc_version(void) { return 200; }
 
 const char* lc_last_error(void) { return g_last_error; }
 

@@ -90,6 +90,28 @@ __device__ __forceinline__ float lc_log2(float x) { return __builtin_amdgcn_logf
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
+// ---------------------------------------------------------------------------
+// Additive attention bias (an additive attention mask added to the scaled
+// scores), taken into the exp2 domain. Entries below kBiasFloor (and NaN) act
+// as kBiasFloor: such a key keeps zero weight next to any real score, and a
+// row whose visible keys all carry such values averages them uniformly, as
+// the softmax of equal scores does (the usual finfo.min padding masks);
+// -inf excludes the key exactly.
+// ---------------------------------------------------------------------------
+constexpr float kBiasFloor = -1.0e30f;
+
+__device__ __forceinline__ float lc_bias_log2(float b) {
+  return b == -INFINITY ? -INFINITY : fmaxf(b, kBiasFloor) * 1.4426950408889634f;
+}
+
+// One bias element of run-time dtype (LC_DTYPE_*) at element offset off.
+__device__ __forceinline__ float lc_load_bias(const void* p, int64_t off, int dtype) {
+  if (dtype == LC_DTYPE_F32) return static_cast<const float*>(p)[off];
+  const uint16_t bits = static_cast<const uint16_t*>(p)[off];
+  if (dtype == LC_DTYPE_BF16) return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+  return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
 // Wave64 reductions (ds_swizzle / DPP via __shfl_xor).
 __device__ __forceinline__ float lc_wave_sum(float v) {
 #pragma unroll

@@ -22,7 +22,9 @@
 //      the MFMA k index is mapped to tokens so that the S^T accumulator
 //      registers ARE the P^T operand.
 // Each split writes o/l (fp32) and its log2-domain logsumexp; the merge
-// kernel combines splits with weights 2^(lse_s - lse).
+// kernel combines splits with weights 2^(lse_s - lse). An optional additive
+// bias per (sequence, query head, token) (an attention mask) is added to the
+// scaled scores.
 #include <math.h>
 
 #include <mutex>
@@ -46,7 +48,19 @@ struct DecodeArgs {
   float* part_lse;  // [B*Hq, max_splits], log2 domain
   int B, Hq, Hkv, G, D, P, p_shift, split_tokens, max_splits, n_hgroups;
   float scale_log2;
+  // Additive bias: element (b, h, t) at bias[b*bias_sb + h*bias_sh + t] for
+  // t < bias_len (tokens past bias_len get none); dtype bias_dtype; null: none.
+  const void* bias;
+  int64_t bias_sb, bias_sh;
+  int bias_len, bias_dtype;
 };
+
+// Bias of token tok for (b, h), in the exp2 domain; 0 past bias_len.
+__device__ __forceinline__ float decode_bias(const DecodeArgs& a, int b, int h, int tok) {
+  return tok < a.bias_len
+             ? lc_bias_log2(lc_load_bias(a.bias, b * a.bias_sb + h * a.bias_sh + tok, a.bias_dtype))
+             : 0.f;
+}
 
 __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
   int len = a.seq_lens[b];
@@ -221,8 +235,9 @@ __device__ __forceinline__ void store_partial(const DecodeArgs& a, int b, int h,
   if (q4 == 0) a.part_lse[pidx] = l_tot > 0.f ? m_ref + lc_log2(l_tot) : -INFINITY;
 }
 
-// Main kernel: page_size % 32 == 0 (every step inside one page).
-template <typename T, int DPAD>
+// Main kernel: page_size % 32 == 0 (every step inside one page). HB: the call
+// carries an additive bias (loaded with the step's K/V, one step ahead).
+template <typename T, int DPAD, bool HB>
 __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   typedef MfmaOps<T> Ops;
   typedef typename Ops::v8 v8;
@@ -276,6 +291,19 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   float l_lane = 0.f;
 
   u32x4_t sk[NI], sv[NI];
+  // Bias of this lane's scores of the step at t: tokens t + gi*16 + q4*4 + i.
+  float bnx[2][4];
+  auto issue_bias = [&](int t) __attribute__((always_inline)) {
+    if constexpr (HB) {
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tok = t + gi * 16 + q4 * 4 + i;
+          bnx[gi][i] = head_ok && tok < t_end ? decode_bias(a, b, h, tok) : 0.f;
+        }
+    }
+  };
   // Issue the loads of the step starting at t. Past the split end (the
   // prefetch after the last step) every offset is out of range: zeros, no
   // memory traffic, and no branch for the wait-count bookkeeping to merge.
@@ -307,6 +335,7 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   };
 
   bool pvalid = issue(t_begin);
+  issue_bias(t_begin);
   for (int t = t_begin; t < t_end; t += kStep) {
     // staging -> LDS (row-major [32 tok][LROW])
 #pragma unroll
@@ -315,8 +344,16 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
       *reinterpret_cast<u32x4_t*>(lds_k + row * LROW + schunk * 8) = sk[i];
       *reinterpret_cast<u32x4_t*>(lds_v + row * LROW + schunk * 8) = sv[i];
     }
+    float bcu[2][4];
+    if constexpr (HB) {
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bcu[gi][i] = bnx[gi][i];
+    }
     const bool cur_valid = pvalid;
     pvalid = issue(t + kStep);
+    if (t + kStep < t_end) issue_bias(t + kStep);
     lc_compiler_fence();
 
     f32x4_t sacc[2];
@@ -335,7 +372,9 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool live = cur_valid && t + gi * 16 + q4 * 4 + i < t_end;
-        sc[gi][i] = live ? sacc[gi][i] * a.scale_log2 : -INFINITY;
+        const float x = HB ? fmaf(sacc[gi][i], a.scale_log2, bcu[gi][i])
+                           : sacc[gi][i] * a.scale_log2;
+        sc[gi][i] = live ? x : -INFINITY;
       }
     const v8 pop = softmax_step<T, DT>(sc, m_ref, l_lane, o);
     pv_step<T, DT, LROW>(lds_v, q4, col, pop, o);
@@ -348,7 +387,7 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
 // Three waves per SIMD up to head_dim 128: at 144 VGPRs and 9 KiB of LDS the
 // kernel fits them without spills, and the extra loads in flight measured 6%
 // faster than two. (head_dim 256 would spill at three.)
-template <typename T, int DPAD>
+template <typename T, int DPAD, bool HB>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(DPAD <= 128 ? 3 : 1))) void
 paged_decode_lanes_kernel(DecodeArgs a) {
   typedef MfmaOps<T> Ops;
@@ -411,7 +450,12 @@ paged_decode_lanes_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool live = (r.valid[gi] >> (q4 * 4 + i)) & 1;
-        sc[gi][i] = live ? sacc[gi][i] * a.scale_log2 : -INFINITY;
+        float x = sacc[gi][i] * a.scale_log2;
+        if constexpr (HB) {
+          const int tok = t + gi * 16 + q4 * 4 + i;
+          if (head_ok && live) x += decode_bias(a, b, h, tok);
+        }
+        sc[gi][i] = live ? x : -INFINITY;
       }
     const v8 pop = softmax_step<T, DT>(sc, m_ref, l_lane, o);
     lc_compiler_fence();
@@ -456,7 +500,11 @@ __global__ __launch_bounds__(64) void paged_decode_generic_kernel(DecodeArgs a) 
       const int d = lane + 64 * i;
       if (d < a.D) dot = fmaf(qv[i], lc_to_f32(kp[off + d]), dot);
     }
-    const float s = lc_wave_sum(dot) * a.scale_log2;
+    float s = lc_wave_sum(dot) * a.scale_log2;
+    if (a.bias != nullptr) {
+      s += decode_bias(a, b, h, t);
+      if (s == -INFINITY) continue;  // uniform: every lane reads the same element
+    }
     const float m_new = fmaxf(m_run, s);
     const float alpha = lc_exp2(m_run - m_new);
     const float p = lc_exp2(s - m_new);
@@ -561,10 +609,15 @@ int launch_mfma(const DecodeArgs& a, bool rows, hipStream_t st) {
   // the final, mostly partial splits of the longest sequences rather than
   // full splits of the last sequences, which shortens the ragged tail.
   dim3 grid(a.Hkv * a.n_hgroups, a.B, a.max_splits);
-  if (rows)
-    paged_decode_rows_kernel<T, DPAD><<<grid, 64, 0, st>>>(a);
+  const bool hb = a.bias != nullptr;
+  if (rows && hb)
+    paged_decode_rows_kernel<T, DPAD, true><<<grid, 64, 0, st>>>(a);
+  else if (rows)
+    paged_decode_rows_kernel<T, DPAD, false><<<grid, 64, 0, st>>>(a);
+  else if (hb)
+    paged_decode_lanes_kernel<T, DPAD, true><<<grid, 64, 0, st>>>(a);
   else
-    paged_decode_lanes_kernel<T, DPAD><<<grid, 64, 0, st>>>(a);
+    paged_decode_lanes_kernel<T, DPAD, false><<<grid, 64, 0, st>>>(a);
   return lc_check_launch("lc_paged_decode_fwd (mfma)");
 }
 
@@ -612,7 +665,8 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
                       int64_t kv_s_head, int64_t kv_s_tok, const int32_t* block_table,
                       int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
                       const int32_t* seq_lens, void* out, int64_t o_sb, int64_t o_sh, float* lse,
-                      void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
+                      const void* bias, int64_t bias_sb, int64_t bias_sh, int64_t bias_len,
+                      int bias_dtype, void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
                       int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
                       int64_t max_splits, float scale, int dtype, void* stream) {
   LC_REQUIRE((q && key_pages && value_pages && block_table && seq_lens && out && workspace) ||
@@ -638,6 +692,12 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
   LC_REQUIRE(workspace_bytes >= need, "%s: workspace %lld < %lld bytes", who,
              (long long)workspace_bytes, (long long)need);
   LC_REQUIRE(lc_aligned(workspace, 256), "%s: workspace not 256-byte aligned", who);
+  LC_REQUIRE(bias == nullptr || (bias_sb >= 0 && bias_sh >= 0 && bias_len >= 0 &&
+                                 bias_len < (1LL << 31)),
+             "%s: bad bias strides or length", who);
+  LC_REQUIRE(bias == nullptr || bias_dtype == LC_DTYPE_F32 || bias_dtype == LC_DTYPE_F16 ||
+                 bias_dtype == LC_DTYPE_BF16,
+             "%s: unknown bias dtype %d", who, bias_dtype);
   if (B == 0) return LC_OK;
 
   DecodeArgs a{};
@@ -669,6 +729,11 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
   a.max_splits = static_cast<int>(max_splits);
   a.n_hgroups = 1;
   a.scale_log2 = scale * kLog2e;
+  a.bias = bias_len > 0 ? bias : nullptr;
+  a.bias_sb = bias_sb;
+  a.bias_sh = bias_sh;
+  a.bias_len = static_cast<int>(bias_len);
+  a.bias_dtype = bias_dtype;
 
   const int esz = lc_dtype_size(dtype);
   const bool half = dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16;
@@ -760,15 +825,16 @@ int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                         const void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
                         int64_t kv_s_tok, const int32_t* block_table, int64_t bt_stride,
                         int64_t max_pages_per_seq, int64_t num_pages, const int32_t* seq_lens,
-                        void* out, int64_t o_sb, int64_t o_sh, float* lse, void* workspace,
-                        int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
-                        int64_t page_size, int64_t split_tokens, int64_t max_splits, float scale,
-                        int dtype, void* stream) {
+                        void* out, int64_t o_sb, int64_t o_sh, float* lse, const void* bias,
+                        int64_t bias_sb, int64_t bias_sh, int64_t bias_len, int bias_dtype,
+                        void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
+                        int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
+                        int64_t max_splits, float scale, int dtype, void* stream) {
   return paged_decode_impl("lc_paged_decode_fwd", q, q_sb, q_sh, key_pages, value_pages,
                            kv_s_page, kv_s_head, kv_s_tok, block_table, bt_stride,
-                           max_pages_per_seq, num_pages, seq_lens, out, o_sb, o_sh, lse,
-                           workspace, workspace_bytes, B, Hq, Hkv, D, page_size, split_tokens,
-                           max_splits, scale, dtype, stream);
+                           max_pages_per_seq, num_pages, seq_lens, out, o_sb, o_sh, lse, bias,
+                           bias_sb, bias_sh, bias_len, bias_dtype, workspace, workspace_bytes, B,
+                           Hq, Hkv, D, page_size, split_tokens, max_splits, scale, dtype, stream);
 }
 
 int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
@@ -777,9 +843,10 @@ int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
                                 const int32_t* block_table, int64_t bt_stride,
                                 int64_t max_pages_per_seq, int64_t num_pages,
                                 const int32_t* seq_lens, void* out, int64_t o_sb, int64_t o_sh,
-                                float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
-                                int64_t page_size, int64_t split_tokens, int64_t max_splits,
-                                float scale, int dtype, void* stream) {
+                                float* lse, const void* bias, int64_t bias_sb, int64_t bias_sh,
+                                int64_t bias_len, int bias_dtype, int64_t B, int64_t Hq,
+                                int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
+                                int64_t max_splits, float scale, int dtype, void* stream) {
   static const char* who = "lc_paged_decode_fwd_noalloc";
   if (B == 0) return LC_OK;
   const int64_t need = lc_paged_decode_workspace_bytes(B, Hq, D, max_splits);
@@ -797,8 +864,9 @@ int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
   // partials, and the merge reads only those splits.
   return paged_decode_impl(who, q, q_sb, q_sh, key_pages, value_pages, kv_s_page, kv_s_head,
                            kv_s_tok, block_table, bt_stride, max_pages_per_seq, num_pages,
-                           seq_lens, out, o_sb, o_sh, lse, ws, LC_DECODE_NOALLOC_SCRATCH_BYTES, B,
-                           Hq, Hkv, D, page_size, split_tokens, max_splits, scale, dtype, stream);
+                           seq_lens, out, o_sb, o_sh, lse, bias, bias_sb, bias_sh, bias_len,
+                           bias_dtype, ws, LC_DECODE_NOALLOC_SCRATCH_BYTES, B, Hq, Hkv, D,
+                           page_size, split_tokens, max_splits, scale, dtype, stream);
 }
 
 }  // extern "C"

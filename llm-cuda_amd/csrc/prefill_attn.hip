@@ -7,7 +7,9 @@
 //   * prefill_generic_kernel (everything else, incl. fp32): one lane per query
 //     row, fp32 FMA, K/V tiles staged through LDS.
 // Both compute, for query row i of (b, h) and keys j < Skv with
-// j <= i + q_offset: o = softmax(q.k_j * scale) v, lse = ln-sum-exp.
+// j <= i + q_offset: o = softmax(q.k_j * scale + bias_ij) v, lse = ln-sum-exp,
+// where the optional additive bias (an attention mask) is read through
+// broadcast strides.
 #include <math.h>
 
 #include <type_traits>
@@ -28,6 +30,13 @@ struct PrefillArgs {
   int64_t qs[4], ks[4], vs[4], os[4];
   int B, Hq, Hkv, G, Sq, Skv, D, q_offset;
   float scale_log2;
+  // Additive bias [B, Hq, Sq, Skv] with element strides bs (0 = broadcast);
+  // null: none. bias_dtype is LC_DTYPE_*; bias_vec: the MFMA kernel may read
+  // 4 consecutive keys with one load (see BiasTile).
+  const void* bias;
+  int64_t bs[4];
+  int bias_dtype;
+  int bias_vec;
 };
 
 // ---------------------------------------------------------------------------
@@ -60,6 +69,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
   const int last_row = min(a.Sq - 1, (int)blockIdx.x * 64 + 63);
   const int kv_hi = min(a.Skv, last_row + a.q_offset + 1);
   const int my_hi = row_ok ? min(a.Skv, i + a.q_offset + 1) : 0;
+  const int64_t brow = b * a.bs[0] + h * a.bs[1] + (int64_t)i * a.bs[2];
   float m = -INFINITY, l = 0.f;
 
   for (int j0 = 0; j0 < kv_hi; j0 += KT) {
@@ -78,6 +88,10 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 #pragma unroll
       for (int d = 0; d < DMAX; ++d) s = fmaf(qr[d], ks[r][d], s);
       s *= a.scale_log2;
+      if (a.bias != nullptr) {
+        s += lc_bias_log2(lc_load_bias(a.bias, brow + (int64_t)(j0 + r) * a.bs[3], a.bias_dtype));
+        if (s == -INFINITY) continue;  // key excluded by the mask
+      }
       const float m_new = fmaxf(m, s);
       const float alpha = lc_exp2(m - m_new);
       const float p = lc_exp2(s - m_new);
@@ -136,8 +150,12 @@ constexpr int kPfRows = 32;     // query rows per wave
 constexpr int kPfKeys = 64;     // keys per tile
 constexpr float kPfRescaleLog2 = 8.0f;
 
-template <typename T, int DPAD>
-__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+// With an additive bias (BIAS != 0) the kernel runs one wave per SIMD: the
+// bias tile held one iteration ahead does not fit the two-wave register
+// budget without spills.
+template <typename T, int DPAD, int BIAS>
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((
+    amdgpu_waves_per_eu(BIAS == 0 ? 2 : 1, BIAS == 0 ? 2 : 1))) void
 prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
@@ -197,9 +215,28 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   const int kbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.ks[2] + a.D) * sizeof(T)) : 0;
   const int vbytes = a.Skv > 0 ? static_cast<int>(((int64_t)(a.Skv - 1) * a.vs[2] + a.D) * sizeof(T)) : 0;
 
+  // Additive bias (BIAS != 0): this (b, head)'s slice through one buffer
+  // descriptor; the tile's values are loaded one iteration ahead of the SM1
+  // that adds them (see BiasTile).
+  const int qi = r0 + l32;
+  constexpr int besz = BIAS == 2 ? 4 : 2;
+  BiasTile<T, BIAS == 0 ? 1 : BIAS> btile;
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(static_cast<const char*>(BIAS != 0 ? a.bias : a.q) +
+                        (BIAS != 0 ? (b * a.bs[0] + (int64_t)head * a.bs[1]) * besz : 0)),
+      0,
+      BIAS != 0 ? static_cast<int>(((int64_t)(a.Sq - 1) * a.bs[2] +
+                                     (int64_t)(a.Skv - 1) * a.bs[3] + 1) * besz)
+                : 0,
+      0x00020000);
+  const int brow_b = static_cast<int>((int64_t)qi * a.bs[2] * besz);
+  const int bs3_b = static_cast<int>(a.bs[3] * besz);
+  auto load_bias = [&](int t) __attribute__((always_inline)) {
+    if constexpr (BIAS != 0) btile.load(brs, brow_b, t * kPfKeys, hh, bs3_b, a.bias_vec != 0);
+  };
+
   // Q^T operand registers.
   v8 qop[KS];
-  const int qi = r0 + l32;
   {
     const bool ok = wave_active && qi < a.Sq;
     const T* qrow = qbase + (int64_t)qi * a.qs[2] + hh * (DPAD / 2);
@@ -304,6 +341,13 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   // SM1 of the tile whose raw scores are in snx (keys k0 ..): sets xcu, the
   // running max and row sum; a required rescale of O is left to apply_rescale.
   auto sm1 = [&](int k0, auto mask_c) __attribute__((always_inline)) {
+    if constexpr (BIAS != 0) {
+      // Scores with the bias, in the exp2 domain.
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) snx[kt][r] = fmaf(snx[kt][r], a.scale_log2, btile.log2_at(kt, r));
+    }
     if constexpr (decltype(mask_c)::value) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -313,13 +357,15 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
           if (key > qi + a.q_offset || key >= a.Skv) snx[kt][r] = -INFINITY;
         }
     }
-    // Raw scores are maxed; the scale (> 0) is applied with the shift.
+    // Without a bias raw scores are maxed and the scale (> 0) is applied with
+    // the shift; with one they are already in the exp2 domain.
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, snx[kt][r]);
-    mx = pf_half_max(mx) * a.scale_log2;
+    mx = pf_half_max(mx);
+    if constexpr (BIAS == 0) mx *= a.scale_log2;
     // The reference max only moves when some row's max grew by more than 2^8
     // (exact: O and l always share it).
     rescale = __ballot(mx > m_ref + kPfRescaleLog2) != 0;
@@ -331,7 +377,8 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) xcu[kt][r] = fmaf(snx[kt][r], a.scale_log2, -m_use);
+      for (int r = 0; r < 16; ++r)
+        xcu[kt][r] = BIAS == 0 ? fmaf(snx[kt][r], a.scale_log2, -m_use) : snx[kt][r] - m_use;
   };
   auto sm2 = [&]() __attribute__((always_inline)) {
     // P^T operands: step (kt, jp) takes accumulator rows j = 2jp, 2jp + 1.
@@ -362,6 +409,9 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   auto iteration = [&](int t, auto par_c, auto mask_c) __attribute__((always_inline)) {
     constexpr int PAR = decltype(par_c)::value;
     constexpr auto other = std::integral_constant<int, PAR ^ 1>{};
+    // The bias of tile t+1 (added in this iteration's SM1) is loaded before
+    // the DMA, so that waiting for it does not wait for the DMA too.
+    if (live(t + 1)) load_bias(t + 1);
     if (t + 2 < n_tiles)
       pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(par_c), wave_s, koff, (t + 2) * kstep_b);
     if (t + 1 < n_tiles)
@@ -410,6 +460,7 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
       pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(std::integral_constant<int, 1>{}), wave_s,
                                    koff, kstep_b);
   }
+  if (live(0)) load_bias(0);
   pf_barrier<true>();
   if (live(0)) {
     qk(kbuf(std::integral_constant<int, 0>{}));
@@ -474,6 +525,14 @@ static int gcd_int(int x, int y) {
   return x;
 }
 
+template <typename T, int BIAS>
+void launch_mfma_bias(const PrefillArgs& a, dim3 grid, int hw, int n_rbg, hipStream_t st) {
+  if (a.D <= 64)
+    prefill_mfma_kernel<T, 64, BIAS><<<grid, 64 * kPfWaves, 0, st>>>(a, hw, n_rbg);
+  else
+    prefill_mfma_kernel<T, 128, BIAS><<<grid, 64 * kPfWaves, 0, st>>>(a, hw, n_rbg);
+}
+
 template <typename T>
 int launch_mfma(const PrefillArgs& a, hipStream_t st) {
   const int hw = gcd_int(a.G, kPfWaves);
@@ -483,10 +542,12 @@ int launch_mfma(const PrefillArgs& a, hipStream_t st) {
   const int64_t nwg = (int64_t)n_rbg * a.Hkv * (a.G / hw) * a.B;
   LC_REQUIRE(nwg < (1LL << 31), "lc_prefill_attn_fwd: grid too large");
   dim3 grid(static_cast<unsigned>(nwg));
-  if (a.D <= 64)
-    prefill_mfma_kernel<T, 64><<<grid, 64 * kPfWaves, 0, st>>>(a, hw, n_rbg);
+  if (a.bias == nullptr)
+    launch_mfma_bias<T, 0>(a, grid, hw, n_rbg, st);
+  else if (a.bias_dtype == LC_DTYPE_F32)
+    launch_mfma_bias<T, 2>(a, grid, hw, n_rbg, st);
   else
-    prefill_mfma_kernel<T, 128><<<grid, 64 * kPfWaves, 0, st>>>(a, hw, n_rbg);
+    launch_mfma_bias<T, 1>(a, grid, hw, n_rbg, st);
   return lc_check_launch("lc_prefill_attn_fwd (mfma)");
 }
 
@@ -512,6 +573,7 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D,
                         const int64_t* q_strides, const int64_t* k_strides,
                         const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
+                        const void* bias, const int64_t* bias_strides, int bias_dtype,
                         float scale, int dtype, void* stream) {
   LC_REQUIRE(q_strides && k_strides && v_strides && o_strides,
              "lc_prefill_attn_fwd: null stride array");
@@ -529,6 +591,13 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
              "lc_prefill_attn_fwd: sequence too long");
   LC_REQUIRE(q_strides[3] == 1 && k_strides[3] == 1 && v_strides[3] == 1 && o_strides[3] == 1,
              "lc_prefill_attn_fwd: head_dim stride must be 1");
+  LC_REQUIRE(bias == nullptr || bias_strides != nullptr,
+             "lc_prefill_attn_fwd: bias without bias_strides");
+  LC_REQUIRE(bias == nullptr || bias_dtype == LC_DTYPE_F32 || bias_dtype == dtype,
+             "lc_prefill_attn_fwd: bias dtype must be fp32 or the dtype of q");
+  if (bias != nullptr)
+    for (int i = 0; i < 4; ++i)
+      LC_REQUIRE(bias_strides[i] >= 0, "lc_prefill_attn_fwd: negative bias stride");
   if (B == 0 || Sq == 0) return LC_OK;
 
   PrefillArgs a{};
@@ -552,6 +621,10 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
   a.D = (int)D;
   a.q_offset = (int)q_offset;
   a.scale_log2 = scale * kLog2e;
+  a.bias = Skv > 0 ? bias : nullptr;
+  a.bias_dtype = bias_dtype;
+  if (bias != nullptr)
+    for (int i = 0; i < 4; ++i) a.bs[i] = bias_strides[i];
   hipStream_t st = lc_stream(stream);
   // MFMA path: 16-bit types, D a multiple of 8 up to 128 (padded to 64 or
   // 128), 16-byte aligned rows.
@@ -563,6 +636,18 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
   for (int i = 0; i < 3; ++i)
     mfma = mfma && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 &&
            o_strides[i] % 8 == 0;
+  if (a.bias != nullptr) {
+    // The MFMA kernel reads one (b, head) bias slice through a buffer
+    // descriptor with 32-bit byte offsets, rows up to Sq + 31 and keys up to
+    // Skv + 63 included.
+    const int64_t besz = lc_dtype_size(bias_dtype);
+    const int64_t s2 = a.bs[2], s3 = a.bs[3];
+    mfma = mfma && ((int64_t)(Sq + kPfRows) * s2 + (Skv + kPfKeys) * s3 + 4) * besz < (1LL << 31);
+    // 4-key vector loads: unit key stride, 4-element aligned rows and base, and
+    // Skv a multiple of 4 so no group straddles the end of a row.
+    a.bias_vec = s3 == 1 && Skv % 4 == 0 && s2 % 4 == 0 && a.bs[0] % 4 == 0 &&
+                 a.bs[1] % 4 == 0 && lc_aligned(bias, 4 * besz);
+  }
   switch (dtype) {
     case LC_DTYPE_F32:
       return launch_generic<float>(a, st);

@@ -2,7 +2,8 @@
 //
 // Given the forward's output O and natural-log logsumexp L, and dO:
 //   delta_i = sum_d dO_id O_id                      (attn_bwd_delta_kernel)
-//   P_ij    = exp(s_ij - L_i),  s_ij = q_i.k_j * scale (keys j <= i + q_offset)
+//   P_ij    = exp(s_ij - L_i),  s_ij = q_i.k_j * scale + bias_ij
+//             (keys j <= i + q_offset; bias: the optional additive mask)
 //   dS_ij   = P_ij (dO_i.v_j - delta_i)
 //   dQ_i    = scale * sum_j dS_ij k_j                (one pass over key tiles)
 //   dK_j    = scale * sum_{h in group, i} dS_ij q_i  (one pass over query tiles,
@@ -43,6 +44,12 @@ struct BwdArgs {
   int64_t qs[4], ks[4], vs[4], dos[4], dqs[4], dks[4], dvs[4];
   int B, Hq, Hkv, G, Sq, Skv, D, q_offset;
   float scale, scale_log2;
+  // Additive bias [B, Hq, Sq, Skv] with element strides bs (0 = broadcast),
+  // dtype bias_dtype (LC_DTYPE_*); null: none. bias_vec as in the forward.
+  const void* bias;
+  int64_t bs[4];
+  int bias_dtype;
+  int bias_vec;
 };
 
 // ---------------------------------------------------------------------------
@@ -138,6 +145,7 @@ __global__ __launch_bounds__(64) void attn_bwd_dq_generic_kernel(BwdArgs a) {
   const int kv_hi = min(a.Skv, last_row + a.q_offset + 1);
   // A row with lse = -inf saw no key: its gradient is zero.
   const int my_hi = (row_ok && lse != -INFINITY) ? min(a.Skv, i + a.q_offset + 1) : 0;
+  const int64_t brow = b * a.bs[0] + h * a.bs[1] + (int64_t)i * a.bs[2];
   for (int j0 = 0; j0 < kv_hi; j0 += KT) {
     __syncthreads();
     for (int e = lane; e < KT * DMAX; e += 64) {
@@ -159,7 +167,10 @@ __global__ __launch_bounds__(64) void attn_bwd_dq_generic_kernel(BwdArgs a) {
       }
       s = row_sum<LPR>(s);
       dp = row_sum<LPR>(dp);
-      const float p = lc_exp2(s * a.scale_log2 - lse2);
+      float x = s * a.scale_log2 - lse2;
+      if (a.bias != nullptr)
+        x += lc_bias_log2(lc_load_bias(a.bias, brow + (int64_t)(j0 + r) * a.bs[3], a.bias_dtype));
+      const float p = lc_exp2(x);
       const float ds = p * (dp - dl);
 #pragma unroll
       for (int t = 0; t < 32; ++t) acc[t] = fmaf(ds, ks[r][t * LPR + sub], acc[t]);
@@ -235,7 +246,12 @@ __global__ __launch_bounds__(64) void attn_bwd_dkv_generic_kernel(BwdArgs a) {
         }
         s = row_sum<LPR>(s);
         dp = row_sum<LPR>(dp);
-        const float p = lc_exp2(s * a.scale_log2 - lse_t[r]);
+        float x = s * a.scale_log2 - lse_t[r];
+        if (a.bias != nullptr)
+          x += lc_bias_log2(lc_load_bias(
+              a.bias, b * a.bs[0] + h * a.bs[1] + (int64_t)i * a.bs[2] + (int64_t)j * a.bs[3],
+              a.bias_dtype));
+        const float p = lc_exp2(x);
         const float ds = p * (dp - dl_t[r]);
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
@@ -391,8 +407,11 @@ __device__ __forceinline__ void store_transposed(T* out, const f32x16_t (&acc)[D
 // K and V tiles are double-buffered in LDS and fetched by buffer-to-LDS DMA
 // one tile ahead.
 // ---------------------------------------------------------------------------
-template <typename T, int DPAD>
-__global__ __launch_bounds__(64 * kBwWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+// With an additive bias (BIAS != 0: 1 = dtype T, 2 = fp32) the kernel runs one
+// wave per SIMD (the bias tile does not fit the two-wave register budget).
+template <typename T, int DPAD, int BIAS>
+__global__ __launch_bounds__(64 * kBwWaves) __attribute__((
+    amdgpu_waves_per_eu(BIAS == 0 ? 2 : 1, BIAS == 0 ? 2 : 1))) void
 attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
@@ -446,6 +465,20 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
   const float lse2 = row_ok ? a.lse2[ridx] : INFINITY;
   const float dl = row_ok ? a.delta[ridx] : 0.f;
 
+  // Additive bias of the tile, loaded before its products (see BiasTile).
+  constexpr int besz = BIAS == 2 ? 4 : 2;
+  BiasTile<T, BIAS == 0 ? 1 : BIAS> btile;
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(static_cast<const char*>(BIAS != 0 ? a.bias : a.q) +
+                        (BIAS != 0 ? (b * a.bs[0] + (int64_t)head * a.bs[1]) * besz : 0)),
+      0,
+      BIAS != 0 ? static_cast<int>(((int64_t)(a.Sq - 1) * a.bs[2] +
+                                     (int64_t)(a.Skv - 1) * a.bs[3] + 1) * besz)
+                : 0,
+      0x00020000);
+  const int brow_b = static_cast<int>((int64_t)qi * a.bs[2] * besz);
+  const int bs3_b = static_cast<int>(a.bs[3] * besz);
+
   const PfLoadOffsets<NIW> koff = tile_dma_offsets<NIW, DPAD, T>(wave, lane, a.ks[2], a.D);
   const PfLoadOffsets<NIW> voff = tile_dma_offsets<NIW, DPAD, T>(wave, lane, a.vs[2], a.D);
   const int kstep_b = static_cast<int>(kBwTile * a.ks[2] * sizeof(T));
@@ -494,6 +527,7 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float x = fmaf(sa[kt][r], a.scale_log2, -lse2);
+        if constexpr (BIAS != 0) x += btile.log2_at(kt, r);
         if constexpr (decltype(mask_c)::value) {
           const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
           if (key > qi + a.q_offset || key >= a.Skv) x = -INFINITY;
@@ -521,11 +555,15 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
   // other pair; the closing barrier publishes it and frees buffers PAR.
   auto iteration = [&](int t, auto par_c, auto mask_c) __attribute__((always_inline)) {
     constexpr auto other = std::integral_constant<int, decltype(par_c)::value ^ 1>{};
+    const bool work = wave_active && t * kBwTile < my_kv_end;
+    // Bias before the DMA: waiting for it does not wait for the DMA.
+    if constexpr (BIAS != 0)
+      if (work) btile.load(brs, brow_b, t * kBwTile, hh, bs3_b, a.bias_vec != 0);
     if (t + 1 < n_tiles) {
       pf_dma_tile<NIW, RPI, ROW_B>(kbase, kbytes, kbuf(other), wave_s, koff, (t + 1) * kstep_b);
       pf_dma_tile<NIW, RPI, ROW_B>(vbase, vbytes, vbuf(other), wave_s, voff, (t + 1) * vstep_b);
     }
-    if (wave_active && t * kBwTile < my_kv_end) tile(t, kbuf(par_c), vbuf(par_c), mask_c);
+    if (work) tile(t, kbuf(par_c), vbuf(par_c), mask_c);
     pf_barrier<true>();
   };
 
@@ -579,7 +617,9 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
 // Q, dO, lse2 and delta tiles are double-buffered in LDS, fetched by DMA one
 // tile ahead. Blocks are dispatched heaviest (earliest keys) first.
 // ---------------------------------------------------------------------------
-template <typename T, int DPAD>
+// BIAS: 0 none, 1 = dtype T, 2 = fp32. Queries sit on accumulator rows here,
+// so a lane's bias values (one key, 32 query rows) are read one element each.
+template <typename T, int DPAD, int BIAS>
 __global__ __launch_bounds__(64 * kBkWaves) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 attn_bwd_dkv_mfma_kernel(BwdArgs a) {
   typedef Mfma32<T> Ops;
@@ -682,6 +722,41 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a) {
                                              qt * kBwTile * 4, 0, 0);
   };
 
+  // Bias of the tile of iteration `it`: query rows qt*64 + h2*32 + 8j + 4hh + i
+  // of head g, this lane's key kj (register h2, 4j + i), loaded before the
+  // next tile's DMA and consumed after the tile's S and dP products.
+  float bv[2][16];
+  auto load_bias = [&](int it) __attribute__((always_inline)) {
+    if constexpr (BIAS != 0) {
+      constexpr int besz = BIAS == 2 ? 4 : 2;
+      const int step = it / a.G;
+      const int g = it - step * a.G;
+      const int qt = n_qt - 1 - step;
+      const int h = kvh * a.G + g;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(static_cast<const char*>(a.bias) +
+                            (b * a.bs[0] + (int64_t)h * a.bs[1]) * besz),
+          0,
+          static_cast<int>(((int64_t)(a.Sq - 1) * a.bs[2] + (int64_t)(a.Skv - 1) * a.bs[3] + 1) *
+                           besz),
+          0x00020000);
+      const int col_b = static_cast<int>((int64_t)kj * a.bs[3] * besz);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = qt * kBwTile + h2 * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+          const int off = static_cast<int>((int64_t)row * a.bs[2] * besz) + col_b;
+          if constexpr (BIAS == 2) {
+            bv[h2][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+          } else {
+            const uint16_t hb = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+            bv[h2][r] = static_cast<float>(__builtin_bit_cast(T, hb));
+          }
+        }
+    }
+  };
+
   auto tile = [&](int qt, auto p_c, auto mask_c) __attribute__((always_inline)) {
     LC_LDS const char* ql = qbuf(p_c);
     LC_LDS const char* ol = obuf(p_c);
@@ -716,6 +791,7 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int r = j * 4 + i;
           float x = fmaf(sa[h2][r], a.scale_log2, -l4[i]);
+          if constexpr (BIAS != 0) x += lc_bias_log2(bv[h2][r]);
           if constexpr (decltype(mask_c)::value) {
             if (kj > qt * kBwTile + row + i + a.q_offset) x = -INFINITY;
           }
@@ -748,6 +824,7 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a) {
 
   auto iteration = [&](int it, auto par_c) __attribute__((always_inline)) {
     constexpr auto other = std::integral_constant<int, decltype(par_c)::value ^ 1>{};
+    if (key0 < a.Skv) load_bias(it);
     if (it + 1 < n_iter) fetch(it + 1, other);
     const int qt = n_qt - 1 - it / a.G;
     if (key0 < a.Skv) {
@@ -786,6 +863,22 @@ static int gcd_int(int x, int y) {
   return x;
 }
 
+template <typename T, int BIAS>
+void launch_dq_mfma(const BwdArgs& a, unsigned nwg, int hw, int n_rbg, hipStream_t st) {
+  if (a.D <= 64)
+    attn_bwd_dq_mfma_kernel<T, 64, BIAS><<<nwg, 64 * kBwWaves, 0, st>>>(a, hw, n_rbg);
+  else
+    attn_bwd_dq_mfma_kernel<T, 128, BIAS><<<nwg, 64 * kBwWaves, 0, st>>>(a, hw, n_rbg);
+}
+
+template <typename T, int BIAS>
+void launch_dkv_mfma(const BwdArgs& a, unsigned nwg, hipStream_t st) {
+  if (a.D <= 64)
+    attn_bwd_dkv_mfma_kernel<T, 64, BIAS><<<nwg, 64 * kBkWaves, 0, st>>>(a);
+  else
+    attn_bwd_dkv_mfma_kernel<T, 128, BIAS><<<nwg, 64 * kBkWaves, 0, st>>>(a);
+}
+
 template <typename T>
 int launch_bwd_mfma(const BwdArgs& a, hipStream_t st) {
   const int hw = gcd_int(a.G, kBwWaves);
@@ -796,17 +889,22 @@ int launch_bwd_mfma(const BwdArgs& a, hipStream_t st) {
   const int n_kb = (a.Skv + kBkKeys - 1) / kBkKeys;
   const int64_t nwg_k = (int64_t)n_kb * a.Hkv * a.B;
   LC_REQUIRE(nwg_q < (1LL << 31) && nwg_k < (1LL << 31), "lc_prefill_attn_bwd: grid too large");
+  const int bias = a.bias == nullptr ? 0 : (a.bias_dtype == LC_DTYPE_F32 ? 2 : 1);
   if (nwg_q > 0) {
-    if (a.D <= 64)
-      attn_bwd_dq_mfma_kernel<T, 64><<<(unsigned)nwg_q, 64 * kBwWaves, 0, st>>>(a, hw, n_rbg);
+    if (bias == 0)
+      launch_dq_mfma<T, 0>(a, (unsigned)nwg_q, hw, n_rbg, st);
+    else if (bias == 1)
+      launch_dq_mfma<T, 1>(a, (unsigned)nwg_q, hw, n_rbg, st);
     else
-      attn_bwd_dq_mfma_kernel<T, 128><<<(unsigned)nwg_q, 64 * kBwWaves, 0, st>>>(a, hw, n_rbg);
+      launch_dq_mfma<T, 2>(a, (unsigned)nwg_q, hw, n_rbg, st);
   }
   if (nwg_k > 0) {
-    if (a.D <= 64)
-      attn_bwd_dkv_mfma_kernel<T, 64><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a);
+    if (bias == 0)
+      launch_dkv_mfma<T, 0>(a, (unsigned)nwg_k, st);
+    else if (bias == 1)
+      launch_dkv_mfma<T, 1>(a, (unsigned)nwg_k, st);
     else
-      attn_bwd_dkv_mfma_kernel<T, 128><<<(unsigned)nwg_k, 64 * kBkWaves, 0, st>>>(a);
+      launch_dkv_mfma<T, 2>(a, (unsigned)nwg_k, st);
   }
   return lc_check_launch("lc_prefill_attn_bwd (mfma)");
 }
@@ -857,6 +955,7 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
                         const int64_t* v_strides, const int64_t* o_strides,
                         const int64_t* do_strides, const int64_t* dq_strides,
                         const int64_t* dk_strides, const int64_t* dv_strides, int64_t q_offset,
+                        const void* bias, const int64_t* bias_strides, int bias_dtype,
                         float scale, void* workspace, int64_t workspace_bytes, int dtype,
                         void* stream) {
   LC_REQUIRE(q_strides && k_strides && v_strides && o_strides && do_strides && dq_strides &&
@@ -878,6 +977,13 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
                  do_strides[3] == 1 && dq_strides[3] == 1 && dk_strides[3] == 1 &&
                  dv_strides[3] == 1,
              "lc_prefill_attn_bwd: head_dim stride must be 1");
+  LC_REQUIRE(bias == nullptr || bias_strides != nullptr,
+             "lc_prefill_attn_bwd: bias without bias_strides");
+  LC_REQUIRE(bias == nullptr || bias_dtype == LC_DTYPE_F32 || bias_dtype == dtype,
+             "lc_prefill_attn_bwd: bias dtype must be fp32 or the dtype of q");
+  if (bias != nullptr)
+    for (int i = 0; i < 4; ++i)
+      LC_REQUIRE(bias_strides[i] >= 0, "lc_prefill_attn_bwd: negative bias stride");
   const int64_t need = lc_prefill_attn_bwd_workspace_bytes(B, Hq, Sq);
   LC_REQUIRE(workspace_bytes >= need, "lc_prefill_attn_bwd: workspace %lld < %lld bytes",
              (long long)workspace_bytes, (long long)need);
@@ -913,6 +1019,10 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
   a.q_offset = (int)q_offset;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
+  a.bias = Skv > 0 ? bias : nullptr;
+  a.bias_dtype = bias_dtype;
+  if (bias != nullptr)
+    for (int i = 0; i < 4; ++i) a.bs[i] = bias_strides[i];
   float* delta = static_cast<float*>(workspace);
   float* lse2 = delta + need / 8;
   const int64_t esz = lc_dtype_size(dtype);
@@ -927,6 +1037,16 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
          (Skv * v_strides[2] + D) * esz < (1LL << 31) &&
          (Sq * q_strides[2] + D) * esz < (1LL << 31) &&
          (Sq * do_strides[2] + D) * esz < (1LL << 31) && Sq * 4 < (1LL << 31);
+  if (a.bias != nullptr) {
+    // One (b, head) bias slice per buffer descriptor (32-bit byte offsets over
+    // rows up to Sq + 63 and keys up to Skv + 127); 4-key vector loads as in
+    // the forward.
+    const int64_t besz = lc_dtype_size(bias_dtype);
+    const int64_t s2 = a.bs[2], s3 = a.bs[3];
+    mfma = mfma && ((int64_t)(Sq + kBwTile) * s2 + (Skv + kBkKeys) * s3 + 4) * besz < (1LL << 31);
+    a.bias_vec = s3 == 1 && Skv % 4 == 0 && s2 % 4 == 0 && a.bs[0] % 4 == 0 &&
+                 a.bs[1] % 4 == 0 && lc_aligned(bias, 4 * besz);
+  }
   hipStream_t st = lc_stream(stream);
   switch (dtype) {
     case LC_DTYPE_F32:

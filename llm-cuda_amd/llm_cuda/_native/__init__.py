@@ -56,14 +56,15 @@ _SIGNATURES = {
     "lc_prefill_attn_fwd": (
         ctypes.c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p,
-         _c_i64p, _c_i64p, _c_i64p, _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
+         _c_i64p, _c_i64p, _c_i64p, _c_i64, _c_p, _c_i64p, ctypes.c_int, ctypes.c_float,
+         ctypes.c_int, _c_p],
     ),
     "lc_prefill_attn_bwd_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "lc_prefill_attn_bwd": (
         ctypes.c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_i64p,
-         _c_i64, ctypes.c_float, _c_p, _c_i64, ctypes.c_int, _c_p],
+         _c_i64, _c_p, _c_i64p, ctypes.c_int, ctypes.c_float, _c_p, _c_i64, ctypes.c_int, _c_p],
     ),
     "lc_lm_head_argmax_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "lc_lm_head_argmax": (
@@ -75,14 +76,15 @@ _SIGNATURES = {
     "lc_paged_decode_fwd": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
-         _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-         _c_i64, _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
+         _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_p,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
+         ctypes.c_int, _c_p],
     ),
     "lc_paged_decode_fwd_noalloc": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
-         _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-         _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
+         _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
     ),
     "lc_paged_kv_append": (
         ctypes.c_int,

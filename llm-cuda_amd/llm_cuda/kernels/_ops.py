@@ -248,10 +248,61 @@ def _rope(x1: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
 
 
 # ---------------------------------------------------------------------------
+# Additive attention masks
+# ---------------------------------------------------------------------------
+def _mask_dtype(mask: torch.Tensor, data_dtype: torch.dtype) -> torch.Tensor:
+    """An additive mask in a dtype the kernels read: fp32 or the data dtype
+    (other floating dtypes are widened to fp32; non-float masks are refused,
+    since the reference adds the mask to the scores)."""
+    if not mask.is_floating_point():
+        raise TypeError(f"attention_mask must be a floating-point additive mask, got {mask.dtype}")
+    if mask.dtype not in (torch.float32, data_dtype):
+        mask = mask.float()
+    return mask
+
+
+def prefill_bias(mask: torch.Tensor, B: int, Hq: int, Sq: int, Skv: int,
+                 data_dtype: torch.dtype) -> torch.Tensor:
+    """The additive mask as a [B, Hq, Sq, Skv] view (broadcast dimensions get
+    stride 0; nothing is copied unless the dtype must change)."""
+    mask = _mask_dtype(mask, data_dtype)
+    try:
+        return mask.expand(B, Hq, Sq, Skv)
+    except RuntimeError as exc:
+        raise ValueError(f"attention_mask of shape {tuple(mask.shape)} does not broadcast to "
+                         f"[batch, heads, q_len, kv_len] = {(B, Hq, Sq, Skv)}") from exc
+
+
+def decode_bias(mask: torch.Tensor, B: int, Hq: int, data_dtype: torch.dtype) -> torch.Tensor:
+    """The additive mask of one query token as a [B, Hq, L] view with unit token
+    stride (L = the mask's last dimension); accepts [.., 1, L] and [.., L] forms
+    broadcastable to [B, Hq, 1, L]."""
+    mask = _mask_dtype(mask, data_dtype)
+    if mask.dim() == 4:
+        if mask.shape[2] != 1:
+            raise ValueError(f"a decode mask has one query row, got shape {tuple(mask.shape)}")
+        mask = mask[:, :, 0]
+    L = mask.shape[-1]
+    try:
+        m = mask.expand(B, Hq, L)
+    except RuntimeError as exc:
+        raise ValueError(f"attention_mask of shape {tuple(mask.shape)} does not broadcast to "
+                         f"[batch, heads, kv_len] = {(B, Hq, L)}") from exc
+    if L > 1 and m.stride(-1) != 1:
+        m = m.contiguous()
+    return m
+
+
+# ---------------------------------------------------------------------------
 # Prefill attention  (reference: kernels/triton/attention.py:323-378,501-535)
 # ---------------------------------------------------------------------------
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offset: int = 0,
-                      scale: float | None = None, return_lse: bool = False):
+                      scale: float | None = None, return_lse: bool = False,
+                      attention_mask: torch.Tensor | None = None):
+    """Causal attention of q [B, Hq, Sq, D] over k, v [B, Hkv, Skv, D]; key j is
+    visible to query i iff j <= i + q_offset. attention_mask: an additive mask
+    broadcastable to [B, Hq, Sq, Skv] (fp32 or q's dtype), added to the scaled
+    scores as in the reference's torch path (attention.py:457-477)."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be [batch, heads, seq, head_dim]")
     if k.shape != v.shape:
@@ -270,6 +321,10 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offse
     v = v if v.stride(-1) == 1 else v.contiguous()
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    bias = None
+    if attention_mask is not None:
+        nat.require_device(q, attention_mask)
+        bias = prefill_bias(attention_mask, B, Hq, Sq, Skv, q.dtype)
     out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=dev)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=dev) if return_lse else None
     lib = nat.load()
@@ -278,18 +333,22 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offse
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
             None if lse is None else lse.data_ptr(), B, Hq, Hkv, Sq, Skv, D,
             _i64arr(q.stride()), _i64arr(k.stride()), _i64arr(v.stride()), _i64arr(out.stride()),
-            int(q_offset), float(scale), nat.lc_dtype(q), _stream(dev))
+            int(q_offset), None if bias is None else bias.data_ptr(),
+            None if bias is None else _i64arr(bias.stride()),
+            0 if bias is None else nat.lc_dtype(bias), float(scale), nat.lc_dtype(q), _stream(dev))
     nat.check(rc, "lc_prefill_attn_fwd")
     return (out, lse) if return_lse else out
 
 
 def prefill_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
-                               q_offset: int = 0, scale: float | None = None):
+                               q_offset: int = 0, scale: float | None = None,
+                               attention_mask: torch.Tensor | None = None):
     """(dq, dk, dv) of causal attention (reference: kernels/triton/attention.py:380-454).
 
-    `out` and `lse` are the forward's output and fp32 natural-log logsumexp.
-    dk and dv are summed over the query heads that share a kv head.
+    `out` and `lse` are the forward's output and fp32 natural-log logsumexp,
+    computed with the same attention_mask (which gets no gradient). dk and dv
+    are summed over the query heads that share a kv head.
     """
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be [batch, heads, seq, head_dim]")
@@ -312,6 +371,10 @@ def prefill_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     lse = lse.contiguous()
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    bias = None
+    if attention_mask is not None:
+        nat.require_device(q, attention_mask)
+        bias = prefill_bias(attention_mask, B, Hq, Sq, Skv, q.dtype)
     dq = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=dev)
     dk = torch.empty((B, Hkv, Skv, D), dtype=q.dtype, device=dev)
     dv = torch.empty((B, Hkv, Skv, D), dtype=q.dtype, device=dev)
@@ -324,8 +387,11 @@ def prefill_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
             dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, Sq, Skv, D,
             _i64arr(q.stride()), _i64arr(k.stride()), _i64arr(v.stride()),
             _i64arr(out.stride()), _i64arr(dout.stride()), _i64arr(dq.stride()),
-            _i64arr(dk.stride()), _i64arr(dv.stride()), int(q_offset), float(scale),
-            ws.data_ptr(), ws.numel(), nat.lc_dtype(q), _stream(dev))
+            _i64arr(dk.stride()), _i64arr(dv.stride()), int(q_offset),
+            None if bias is None else bias.data_ptr(),
+            None if bias is None else _i64arr(bias.stride()),
+            0 if bias is None else nat.lc_dtype(bias), float(scale), ws.data_ptr(), ws.numel(),
+            nat.lc_dtype(q), _stream(dev))
     nat.check(rc, "lc_prefill_attn_bwd")
     return dq, dk, dv
 
@@ -393,14 +459,17 @@ def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens
 def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
                  block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None = None,
                  return_lse: bool = False, split_tokens: int | None = None,
-                 workspace: torch.Tensor | None = None):
+                 workspace: torch.Tensor | None = None,
+                 attention_mask: torch.Tensor | None = None):
     """One-token GQA attention per sequence over a paged K/V pool (forward only).
 
     q: [B, Hq, 1, D] or [B, Hq, D]; key_pages, value_pages: [N, Hkv, P, D];
-    block_table: int32 [B, max_pages]; seq_lens: int32 [B]. Returns out with
-    q's shape (and lse [B, Hq] fp32 if return_lse).
+    block_table: int32 [B, max_pages]; seq_lens: int32 [B]. attention_mask:
+    additive scores for the query token, broadcastable to [B, Hq, 1, L] (or
+    [B, Hq, L]); token t < L of a sequence gets mask[..., t], later tokens
+    none. Returns out with q's shape (and lse [B, Hq] fp32 if return_lse).
     """
-    args = (block_table, seq_lens, scale, return_lse, split_tokens, workspace)
+    args = (block_table, seq_lens, scale, return_lse, split_tokens, workspace, attention_mask)
     if _records_grad(q, key_pages, value_pages):
         return _ForwardOnly.apply("paged_decode", lambda a, k, v: _paged_decode(a, k, v, *args),
                                   q, key_pages, value_pages)
@@ -409,7 +478,8 @@ def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Te
 
 def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
                   block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None,
-                  return_lse: bool, split_tokens: int | None, workspace: torch.Tensor | None):
+                  return_lse: bool, split_tokens: int | None, workspace: torch.Tensor | None,
+                  attention_mask: torch.Tensor | None = None):
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
     if q4.dim() != 4 or q4.shape[2] != 1:
@@ -453,6 +523,10 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
     need = lib.lc_paged_decode_workspace_bytes(B, Hq, D, max_splits)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+    bias = None
+    if attention_mask is not None:
+        nat.require_device(q4, attention_mask)
+        bias = decode_bias(attention_mask, B, Hq, q4.dtype)
     out = torch.empty((B, Hq, 1, D), dtype=q4.dtype, device=dev)
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
     with _DeviceGuard(dev):
@@ -461,7 +535,10 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
             value_pages.data_ptr(), key_pages.stride(0), key_pages.stride(1),
             key_pages.stride(2), block_table.data_ptr(), block_table.stride(0), maxp, N,
             seq_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
-            None if lse is None else lse.data_ptr(), workspace.data_ptr(),
+            None if lse is None else lse.data_ptr(),
+            None if bias is None else bias.data_ptr(), 0 if bias is None else bias.stride(0),
+            0 if bias is None else bias.stride(1), 0 if bias is None else bias.shape[-1],
+            0 if bias is None else nat.lc_dtype(bias), workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, P, split_tokens,
             max_splits, float(scale), nat.lc_dtype(q4), _stream(dev))
     nat.check(rc, "lc_paged_decode_fwd")

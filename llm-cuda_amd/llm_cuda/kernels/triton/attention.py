@@ -1,7 +1,8 @@
 """Causal prefill attention entry (reference: kernels/triton/attention.py:480-535).
 
-`triton_fused_causal_attention(q, k, v)` computes softmax(q k^T / sqrt(D) +
-causal) v on the lc_prefill_attn_fwd HIP kernel. Differences from the
+`triton_fused_causal_attention(q, k, v, attention_mask)` computes
+softmax(q k^T / sqrt(D) + causal + attention_mask) v on the lc_prefill_attn_fwd
+HIP kernel. Differences from the
 reference, all widening the accepted inputs:
   * GQA is native: k and v may carry fewer heads than q (n_heads a multiple
     of n_kv_heads); the reference required q.shape == k.shape and its callers
@@ -11,12 +12,16 @@ reference, all widening the accepted inputs:
   * `q_offset` shifts the causal diagonal for queries that continue a cached
     prefix (key j is visible to query i iff j <= i + q_offset), the masking of
     models/llama3/attention.py:63-89.
-Additive attention masks are not supported and raise NotImplementedError.
+  * `attention_mask`, the reference's additive mask (broadcastable to
+    [B, H, Sq, Skv], fp32 or q's dtype), is added to the scaled scores inside
+    the kernel, as the reference's torch path does (attention.py:457-477). A
+    row whose visible keys are all at -inf gives zeros (the reference: NaN).
 
 Autograd: when any of q, k, v requires grad, the call goes through
 `_FusedCausalAttentionFunction` (reference: attention.py:323-454), whose
-backward runs lc_prefill_attn_bwd on the saved q, k, v, output and logsumexp.
-The returned lse is not differentiable.
+backward runs lc_prefill_attn_bwd on the saved q, k, v, output, logsumexp and
+mask. The returned lse and the mask get no gradient (a mask that requires
+grad is refused).
 """
 from __future__ import annotations
 
@@ -76,7 +81,10 @@ def can_use_triton_fused_attention(
     v: torch.Tensor,
     attention_mask: torch.Tensor | None = None,
 ) -> bool:
-    if attention_mask is not None:
+    """Whether the HIP kernel takes the call (reference predicate: attention.py:
+    480-498). Additive float masks on the same device are taken as well."""
+    if attention_mask is not None and not (attention_mask.is_floating_point()
+                                           and attention_mask.device == q.device):
         return False
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         return False
@@ -93,21 +101,22 @@ def can_use_triton_fused_attention(
 
 class _FusedCausalAttentionFunction(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, q_offset: int):
-        out, lse = _ops.prefill_attention(q, k, v, q_offset=q_offset, return_lse=True)
-        ctx.save_for_backward(q, k, v, out, lse)
+    def forward(ctx, q, k, v, q_offset: int, mask):
+        out, lse = _ops.prefill_attention(q, k, v, q_offset=q_offset, return_lse=True,
+                                          attention_mask=mask)
+        ctx.save_for_backward(q, k, v, out, lse, mask)
         ctx.q_offset = q_offset
         ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, _dlse):
-        q, k, v, out, lse = ctx.saved_tensors
+        q, k, v, out, lse, mask = ctx.saved_tensors
         if dout is None:
             dout = torch.zeros_like(out)
         dq, dk, dv = _ops.prefill_attention_backward(q, k, v, out, lse, dout,
-                                                     q_offset=ctx.q_offset)
-        return dq, dk, dv, None
+                                                     q_offset=ctx.q_offset, attention_mask=mask)
+        return dq, dk, dv, None, None
 
 
 def triton_fused_causal_attention(
@@ -119,14 +128,17 @@ def triton_fused_causal_attention(
     return_lse: bool = False,
     q_offset: int = 0,
 ):
-    """Causal attention for q [B, Hq, S, D], k/v [B, Hkv, Skv, D]."""
+    """Causal attention for q [B, Hq, S, D], k/v [B, Hkv, Skv, D] with an optional
+    additive attention_mask (reference: kernels/triton/attention.py:501-535)."""
     if not _gqa_compatible(q, k, v):
         raise ValueError(
             "q, k, v must be [batch, heads, seq, head_dim] with matching batch/head_dim and "
             "n_heads a multiple of n_kv_heads")
-    if attention_mask is not None:
-        raise NotImplementedError("additive attention masks are not supported by the HIP kernel")
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
-        out, lse = _FusedCausalAttentionFunction.apply(q, k, v, int(q_offset))
+        if attention_mask is not None and attention_mask.requires_grad:
+            raise NotImplementedError(
+                "attention_mask requires grad; the HIP backward gives the mask no gradient")
+        out, lse = _FusedCausalAttentionFunction.apply(q, k, v, int(q_offset), attention_mask)
         return (out, lse) if return_lse else out
-    return _ops.prefill_attention(q, k, v, q_offset=q_offset, return_lse=return_lse)
+    return _ops.prefill_attention(q, k, v, q_offset=q_offset, return_lse=return_lse,
+                                  attention_mask=attention_mask)

@@ -11,7 +11,9 @@
   batch-1 cache, models/llama3/kv_cache.py:43-44,65-83).
 
 Both return out shaped like q; `return_lse=True` adds the fp32 natural-log
-logsumexp [B, Hq] of the scaled scores.
+logsumexp [B, Hq] of the scaled scores. The paged entry also takes the
+reference's additive attention_mask (the reference's decode predicate refuses
+masks and falls back to torch; that predicate keeps its answer here).
 """
 from __future__ import annotations
 
@@ -105,7 +107,12 @@ def paged_decode_attention(
     return_lse: bool = False,
     split_tokens: int | None = None,
     workspace: torch.Tensor | None = None,
+    attention_mask: torch.Tensor | None = None,
 ):
+    """attention_mask: the reference's additive mask for the query token,
+    broadcastable to [B, Hq, 1, L]; token t < L of each sequence gets
+    mask[..., t] added to its scaled score (models/llama3/attention.py:85-86),
+    later tokens none."""
     return _ops.paged_decode(q, key_pages, value_pages, block_table, seq_lens, scale=scale,
                              return_lse=return_lse, split_tokens=split_tokens,
-                             workspace=workspace)
+                             workspace=workspace, attention_mask=attention_mask)

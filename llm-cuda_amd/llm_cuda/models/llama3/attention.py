@@ -17,6 +17,11 @@ differs only in how the attention itself is computed, all on HIP kernels:
     repeated K/V) and the causal diagonal shifted by the cached prefix length,
     which covers both the reference's fused path (past_len == 0) and its
     `_torch_attention` path with `past_len` (attention.py:63-89,144-147).
+  * An additive attention_mask (broadcastable to [B, H, q_len, kv_len], as the
+    reference adds it to the scores, attention.py:85-86) goes into the same
+    kernels: the prefill kernel for prompts and chunks, the paged decode
+    kernel for one token against the paged cache, and the prefill kernel at
+    the cached offset for one token against a tuple cache.
 """
 from __future__ import annotations
 
@@ -80,6 +85,18 @@ class Llama3Attention(nn.Module):
             cache = self._rope_cache = (key, cap, cos, sin)
         return cache[2][past_len:need], cache[3][past_len:need]
 
+    def _check_mask(self, mask: torch.Tensor, bsz: int, q_len: int, kv_len: int) -> None:
+        """The reference adds the mask to scores [B, H, q_len, kv_len]
+        (attention.py:85-86): refuse what that add would refuse."""
+        try:
+            shape = torch.broadcast_shapes(tuple(mask.shape), (bsz, self.num_heads, q_len, kv_len))
+        except RuntimeError as exc:
+            raise ValueError(f"attention_mask of shape {tuple(mask.shape)} does not broadcast to "
+                             f"{(bsz, self.num_heads, q_len, kv_len)}") from exc
+        if shape != (bsz, self.num_heads, q_len, kv_len):
+            raise ValueError(f"attention_mask of shape {tuple(mask.shape)} does not broadcast to "
+                             f"{(bsz, self.num_heads, q_len, kv_len)}")
+
     def _shape(self, x: torch.Tensor, heads: int) -> torch.Tensor:
         bsz, seq_len, _ = x.shape
         return x.view(bsz, seq_len, heads, self.head_dim).transpose(1, 2)
@@ -91,9 +108,6 @@ class Llama3Attention(nn.Module):
         past_key_value: tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None = None,
         use_cache: bool = False,
     ) -> tuple[torch.Tensor, tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None]:
-        if attention_mask is not None:
-            raise NotImplementedError(
-                "additive attention masks are not supported by the HIP attention kernels")
         bsz, seq_len, _ = x.shape
 
         if FusedLinearWeights.usable(self.q_proj, self.k_proj, self.v_proj):
@@ -119,45 +133,56 @@ class Llama3Attention(nn.Module):
             # Decode step: RoPE and the cache append in one launch, positions
             # taken from the cache's device-side lengths.
             cache = past_key_value
+            if attention_mask is not None:
+                self._check_mask(attention_mask, bsz, 1, past_len + 1)
             rows = cache.max_pages * cache.page_size
             self._rope_tables(0, rows, x.device, x.dtype)
             cos_t, sin_t = self._rope_cache[2], self._rope_cache[3]
             q = cache.append_rotated(q, k, v, cos_t, sin_t)
             out = paged_decode_attention(
-                q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens)
+                q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens,
+                attention_mask=attention_mask)
             out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
             return self.o_proj(out), cache
 
         cos, sin = self._rope_tables(past_len, seq_len, x.device, x.dtype)
         q, k = apply_rotary(q, k, cos, sin)
 
+        mask = attention_mask
         if paged:
             cache = past_key_value
             if use_cache:
                 cache.append(k, v)
             present = cache if use_cache else None
+            if mask is not None:
+                self._check_mask(mask, bsz, seq_len, cache.length if use_cache else past_len)
             if seq_len == 1:
                 # The reference attends to get_kv(): the cache after the
                 # append (or without the new token when use_cache is False).
                 if cache.length == 0:
                     raise ValueError("decode step against an empty cache")
                 out = paged_decode_attention(
-                    q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens)
+                    q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens,
+                    attention_mask=mask)
             elif use_cache and past_len == 0:
-                out = triton_fused_causal_attention(q, k, v)
+                out = triton_fused_causal_attention(q, k, v, attention_mask=mask)
             else:
                 k_all, v_all = cache.get_kv()
-                out = triton_fused_causal_attention(q, k_all, v_all, q_offset=past_len)
+                out = triton_fused_causal_attention(q, k_all, v_all, attention_mask=mask,
+                                                    q_offset=past_len)
         else:
             if past_key_value is not None:
                 past_k, past_v = past_key_value
                 k = torch.cat([past_k, k], dim=-2)
                 v = torch.cat([past_v, v], dim=-2)
             present = (k, v) if use_cache else None
-            if seq_len == 1 and past_len > 0:
+            if mask is not None:
+                self._check_mask(mask, bsz, seq_len, k.shape[-2])
+            if seq_len == 1 and past_len > 0 and mask is None:
                 out = triton_decode_attention(q, k, v)
             else:
-                out = triton_fused_causal_attention(q, k, v, q_offset=past_len)
+                out = triton_fused_causal_attention(q, k, v, attention_mask=mask,
+                                                    q_offset=past_len)
 
         out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
         return self.o_proj(out), present

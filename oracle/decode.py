@@ -19,24 +19,35 @@ import torch
 
 
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                     scale: float | None = None):
-    """q [B, Hq, 1, D]; k, v [B, Hkv, L, D] -> (o fp32 [B, Hq, 1, D], lse fp32 [B, Hq])."""
+                     scale: float | None = None, bias: torch.Tensor | None = None):
+    """q [B, Hq, 1, D]; k, v [B, Hkv, L, D] -> (o fp32 [B, Hq, 1, D], lse fp32 [B, Hq]).
+
+    bias: the reference's additive attention_mask for the query token,
+    broadcastable to [B, Hq, L] (models/llama3/attention.py:85-86 adds it to
+    the scaled scores before the softmax). Rows without a finite score give
+    o = 0, lse = -inf.
+    """
+    from .attention import _softmax_rows
+
     B, Hq, _, D = q.shape
-    Hkv = k.shape[1]
+    Hkv, L = k.shape[1], k.shape[2]
     G = Hq // Hkv
     scale = 1.0 / math.sqrt(D) if scale is None else scale
+    bv = None if bias is None else torch.broadcast_to(bias.float(), (B, Hq, L))
     out = torch.empty((B, Hq, 1, D), dtype=torch.float32)
     lse = torch.empty((B, Hq), dtype=torch.float32)
     for b in range(B):
         for kvh in range(Hkv):
-            qg = q[b, kvh * G:(kvh + 1) * G, 0, :].float()  # [G, D]
+            hs = slice(kvh * G, (kvh + 1) * G)
+            qg = q[b, hs, 0, :].float()                      # [G, D]
             kk = k[b, kvh].float()                           # [L, D]
             vv = v[b, kvh].float()
             s = torch.matmul(qg, kk.t()) * scale             # [G, L]
-            row_lse = torch.logsumexp(s, dim=-1)
-            p = torch.exp(s - row_lse.unsqueeze(-1))
-            out[b, kvh * G:(kvh + 1) * G, 0, :] = torch.matmul(p, vv)
-            lse[b, kvh * G:(kvh + 1) * G] = row_lse
+            if bv is not None:
+                s = s + bv[b, hs]
+            p, row_lse = _softmax_rows(s)
+            out[b, hs, 0, :] = torch.matmul(p, vv)
+            lse[b, hs] = row_lse
     return out, lse
 
 
@@ -64,10 +75,13 @@ def gather_pages_torch(pages: torch.Tensor, block_table: torch.Tensor, length: i
 
 
 def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
-                 block_table: torch.Tensor, seq_lens, scale: float | None = None):
+                 block_table: torch.Tensor, seq_lens, scale: float | None = None,
+                 bias: torch.Tensor | None = None):
     """Per-sequence gather through the block table, then decode_attention.
 
     Empty sequences give o = 0, lse = -inf (the kernel's documented behaviour).
+    bias: [B, Hq or 1, Lb] additive scores of token t < Lb of each sequence
+    (tokens at or past Lb get none).
     """
     B, Hq, _, D = q.shape
     out = torch.zeros((B, Hq, 1, D), dtype=torch.float32)
@@ -80,7 +94,13 @@ def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Te
             continue
         kk = gather_pages_torch(key_pages, bt[b:b + 1], L)
         vv = gather_pages_torch(value_pages, bt[b:b + 1], L)
-        o, l_ = decode_attention(q[b:b + 1], kk, vv, scale)
+        bb = None
+        if bias is not None:
+            row = bias[b:b + 1].float()
+            bb = torch.zeros(1, row.shape[1], L)
+            n = min(L, row.shape[-1])
+            bb[..., :n] = row[..., :n]
+        o, l_ = decode_attention(q[b:b + 1], kk, vv, scale, bias=bb)
         out[b] = o[0]
         lse[b] = l_[0]
     return out, lse

@@ -21,12 +21,15 @@ def _lin(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
 
 
 def forward(state: dict, cfg, input_ids: torch.Tensor, rope_dtype: torch.dtype = torch.float32,
-            inv_freq: torch.Tensor | None = None) -> torch.Tensor:
+            inv_freq: torch.Tensor | None = None,
+            attention_mask: torch.Tensor | None = None) -> torch.Tensor:
     """Full-sequence logits [B, S, vocab] (fp32) for input_ids [B, S].
 
     rope_dtype / inv_freq: dtype of the RoPE tables and the inv_freq buffer of
     the model being checked (a bf16 model builds bf16 tables from a bf16
-    inv_freq, reference rotary.py:61-70).
+    inv_freq, reference rotary.py:61-70). attention_mask: the additive mask
+    every layer adds to its scores (reference model.py:54-107 passes it to
+    each layer; attention.py:85-86 adds it).
     """
     sd = {k: v.detach().cpu() for k, v in state.items()}
     ids = input_ids.cpu()
@@ -42,7 +45,7 @@ def forward(state: dict, cfg, input_ids: torch.Tensor, rope_dtype: torch.dtype =
         v = _lin(h, sd[p + "self_attn.v_proj.weight"]).view(B, S, Hkv, D).transpose(1, 2)
         q = apply_rope(q, cos, sin)
         k = apply_rope(k, cos, sin)
-        o, _ = causal_attention(q, k, v)
+        o, _ = causal_attention(q, k, v, bias=None if attention_mask is None else attention_mask.cpu())
         o = o.transpose(1, 2).reshape(B, S, H * D)
         x = x + _lin(o, sd[p + "self_attn.o_proj.weight"])
         h = rms_norm(x, sd[p + "post_attention_layernorm.weight"], cfg.rms_norm_eps)

@@ -58,21 +58,34 @@ def test_invalid_arguments_rejected_before_launch():
     rc = lib.lc_rmsnorm_fwd(None, None, None, 4, 8, 8, 8, 1e-5, 2, 2, None)
     assert rc == -1 and b"null" in lib.lc_last_error()
     # Hq not a multiple of Hkv
-    rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 5, 3, 4, 4, 16, st, st, st, st, 0, 1.0, 2,
-                                 None)
+    rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 5, 3, 4, 4, 16, st, st, st, st, 0, None,
+                                 None, 0, 1.0, 2, None)
     assert rc == -1 and b"multiple" in lib.lc_last_error()
+    # a bias without strides, or of a third dtype
+    rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 4, 2, 4, 4, 16, st, st, st, st, 0, 8,
+                                 None, 0, 1.0, 2, None)
+    assert rc == -1 and b"bias_strides" in lib.lc_last_error()
+    rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 4, 2, 4, 4, 16, st, st, st, st, 0, 8,
+                                 st, 1, 1.0, 2, None)
+    assert rc == -1 and b"bias dtype" in lib.lc_last_error()
     # odd head_dim for RoPE
     rc = lib.lc_rope_fwd(8, 8, 1, st, st, None, None, 0, None, None, 8, 8, 15, 15, 1, 1, 15, 2,
                          None)
     assert rc == -1 and b"even" in lib.lc_last_error()
     # split does not cover the table capacity
     rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
-                                 256, 1 << 20, 1, 4, 2, 128, 64, 64, 1, 1.0, 2, None)
+                                 None, 0, 0, 0, 0, 256, 1 << 20, 1, 4, 2, 128, 64, 64, 1, 1.0, 2,
+                                 None)
     assert rc == -1 and b"capacity" in lib.lc_last_error()
     # workspace too small
     rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
-                                 256, 16, 1, 4, 2, 128, 64, 64, 4, 1.0, 2, None)
+                                 None, 0, 0, 0, 0, 256, 16, 1, 4, 2, 128, 64, 64, 4, 1.0, 2, None)
     assert rc == -1 and b"workspace" in lib.lc_last_error()
+    # negative bias stride
+    rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
+                                 8, -1, 0, 16, 0, 256, 1 << 20, 1, 4, 2, 128, 64, 64, 4, 1.0, 2,
+                                 None)
+    assert rc == -1 and b"bias" in lib.lc_last_error()
     # unknown dtype
     rc = lib.lc_swiglu_fwd(8, 8, 8, 2, 8, 8, 8, 8, 7, None)
     assert rc == -1 and b"dtype" in lib.lc_last_error()
@@ -215,13 +228,13 @@ def test_empty_extents_accept_null_pointers():
     lib = _native.load()
     st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
     rc = lib.lc_prefill_attn_fwd(None, 8, 8, None, None, 1, 4, 2, 0, 16, 64, st, st, st, st, 0,
-                                 1.0, 2, None)
+                                 None, None, 0, 1.0, 2, None)
     assert rc == 0
-    rc = lib.lc_prefill_attn_fwd(None, 8, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, 1.0,
-                                 2, None)
+    rc = lib.lc_prefill_attn_fwd(None, 8, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, None,
+                                 None, 0, 1.0, 2, None)
     assert rc == -1 and b"null q" in lib.lc_last_error()
-    rc = lib.lc_prefill_attn_fwd(8, None, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, 1.0,
-                                 2, None)
+    rc = lib.lc_prefill_attn_fwd(8, None, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, None,
+                                 None, 0, 1.0, 2, None)
     assert rc == -1 and b"null k" in lib.lc_last_error()
 
 
@@ -239,8 +252,8 @@ def test_every_entry_accepts_empty_work_with_null_pointers():
                            4, 8, 2, None) == 0
     assert lib.lc_lm_head_argmax(None, 8, None, 8, 0, 8, 8, None, None, None, 0, 2, None) == 0
     assert lib.lc_prefill_attn_bwd(None, None, None, None, None, None, None, None, None, 0, 4, 2,
-                                   8, 8, 64, st, st, st, st, st, st, st, st, 0, 1.0, None, 0, 2,
-                                   None) == 0
+                                   8, 8, 64, st, st, st, st, st, st, st, st, 0, None, None, 0, 1.0,
+                                   None, 0, 2, None) == 0
     # a null pointer behind real work is still an error
     assert lib.lc_swiglu_fwd(None, None, None, 2, 8, 8, 8, 8, 2, None) == -1
     assert lib.lc_lm_head_argmax(None, 8, None, 8, 2, 8, 8, None, None, None, 4096, 2, None) == -1

@@ -7,6 +7,14 @@ GQA = per-head attention against kv head h // G, and q_offset equivalence
 (the last rows of a longer prompt). The reference's own CPU parity test
 (tests/test_triton_attention.py:37-47, seed 0, [2,4,8,16], atol 1e-5) is
 reproduced against the brute force.
+
+The additive mask (`bias`, the reference's attention_mask added to the scaled
+scores, attention.py:457-477 and models/llama3/attention.py:85-86) is pinned
+by the brute force with a bias term, the reference's own masked CPU case
+(tests/test_triton_attention.py:78-90), and identities that hold whatever the
+implementation: zero bias changes nothing, a per-row constant shifts only the
+lse, ln 2 on a key equals that key appearing twice, -inf on keys equals
+removing them, and a row whose visible keys all carry finfo.min averages them.
 """
 import math
 
@@ -16,12 +24,13 @@ import torch
 from oracle.attention import causal_attention
 
 
-def brute(q, k, v, q_offset=0):
+def brute(q, k, v, q_offset=0, bias=None):
     B, Hq, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]
     G = Hq // Hkv
     out = torch.zeros(B, Hq, Sq, D, dtype=torch.float64)
     lse = torch.full((B, Hq, Sq), float("-inf"), dtype=torch.float64)
+    bias = None if bias is None else torch.broadcast_to(bias.double(), (B, Hq, Sq, Skv))
     for b in range(B):
         for h in range(Hq):
             kh = h // G
@@ -33,7 +42,7 @@ def brute(q, k, v, q_offset=0):
                     s = 0.0
                     for d in range(D):
                         s += float(q[b, h, i, d]) * float(k[b, kh, j, d])
-                    scores.append(s / math.sqrt(D))
+                    scores.append(s / math.sqrt(D) + (0.0 if bias is None else float(bias[b, h, i, j])))
                 if not scores:
                     continue
                 m = max(scores)
@@ -210,3 +219,120 @@ def test_backward_of_fully_masked_rows_is_zero():
     kv = torch.zeros(1, 1, 0, 8)
     dq, dk, dv = causal_attention_backward(q, kv, kv, torch.randn(1, 2, 3, 8))
     assert torch.equal(dq, torch.zeros_like(dq)) and dk.numel() == 0 and dv.numel() == 0
+
+
+# ---------------------------------------------------------------------------
+# additive mask (bias)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", ["key", "rows", "full"])
+def test_bias_matches_bruteforce(shape):
+    g = torch.Generator().manual_seed(21)
+    B, Hq, Hkv, S, D = 2, 4, 2, 6, 4
+    q = torch.randn(B, Hq, S, D, generator=g)
+    k = torch.randn(B, Hkv, S, D, generator=g)
+    v = torch.randn(B, Hkv, S, D, generator=g)
+    dims = {"key": (B, 1, 1, S), "rows": (1, 1, S, S), "full": (B, Hq, S, S)}[shape]
+    bias = 2.0 * torch.randn(*dims, generator=g)
+    o, lse = causal_attention(q, k, v, bias=bias)
+    ob, lb = brute(q, k, v, bias=bias)
+    assert torch.allclose(o.double(), ob, atol=1e-5)
+    assert torch.allclose(lse.double(), lb, atol=1e-5)
+
+
+def test_reference_masked_cpu_case():
+    """tests/test_triton_attention.py:78-90: seed 1, [1, 2, 6, 8] fp32, a key mask
+    [1, 1, 1, 6] of -1e4 on the last two keys, atol/rtol 1e-5."""
+    torch.manual_seed(1)
+    q = torch.randn(1, 2, 6, 8)
+    k = torch.randn(1, 2, 6, 8)
+    v = torch.randn(1, 2, 6, 8)
+    mask = torch.zeros((1, 1, 1, 6))
+    mask[..., -2:] = -1e4
+    o, _ = causal_attention(q, k, v, bias=mask)
+    ob, _ = brute(q, k, v, bias=mask)
+    assert torch.allclose(o.double(), ob, atol=1e-5, rtol=1e-5)
+    # rows 0..3 never see the masked keys: unchanged by the mask
+    o0, _ = causal_attention(q, k, v)
+    assert torch.equal(o[:, :, :4], o0[:, :, :4])
+
+
+def test_zero_bias_changes_nothing_and_row_constants_shift_lse():
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(1, 4, 9, 8, generator=g)
+    k = torch.randn(1, 2, 9, 8, generator=g)
+    v = torch.randn(1, 2, 9, 8, generator=g)
+    o0, l0 = causal_attention(q, k, v)
+    o1, l1 = causal_attention(q, k, v, bias=torch.zeros(1, 1, 9, 9))
+    assert torch.equal(o0, o1) and torch.equal(l0, l1)
+    c = 5.0 * torch.randn(1, 4, 9, 1, generator=g)
+    o2, l2 = causal_attention(q, k, v, bias=c.expand(1, 4, 9, 9))
+    assert torch.allclose(o2, o0, atol=1e-5)
+    assert torch.allclose(l2, l0 + c[..., 0], atol=1e-5)
+
+
+def test_ln2_bias_equals_a_duplicated_key():
+    """softmax(s + ln 2 on key j) weighs key j as if it appeared twice (every key
+    visible: q_offset >= Skv)."""
+    g = torch.Generator().manual_seed(23)
+    Skv, j = 7, 3
+    q = torch.randn(1, 2, 4, 8, generator=g)
+    k = torch.randn(1, 1, Skv, 8, generator=g)
+    v = torch.randn(1, 1, Skv, 8, generator=g)
+    bias = torch.zeros(1, 1, 1, Skv)
+    bias[..., j] = math.log(2.0)
+    o, lse = causal_attention(q, k, v, q_offset=Skv, bias=bias)
+    kd = torch.cat([k, k[:, :, j:j + 1]], dim=2)
+    vd = torch.cat([v, v[:, :, j:j + 1]], dim=2)
+    od, ld = causal_attention(q, kd, vd, q_offset=Skv + 1)
+    assert torch.allclose(o, od, atol=1e-5) and torch.allclose(lse, ld, atol=1e-5)
+
+
+def test_neg_inf_bias_equals_removed_keys():
+    g = torch.Generator().manual_seed(24)
+    q = torch.randn(2, 2, 5, 8, generator=g)
+    k = torch.randn(2, 2, 8, 8, generator=g)
+    v = torch.randn(2, 2, 8, 8, generator=g)
+    bias = torch.zeros(2, 1, 1, 8)
+    bias[..., 5:] = float("-inf")
+    o, lse = causal_attention(q, k, v, q_offset=8, bias=bias)
+    ot, lt = causal_attention(q, k[:, :, :5], v[:, :, :5], q_offset=8)
+    assert torch.allclose(o, ot, atol=1e-6) and torch.allclose(lse, lt, atol=1e-6)
+    # every key at -inf: no finite score, o = 0 and lse = -inf
+    o, lse = causal_attention(q, k, v, bias=torch.full((1, 1, 1, 8), float("-inf")))
+    assert (o == 0).all() and torch.isinf(lse).all()
+
+
+def test_finfo_min_rows_average_their_visible_keys():
+    """A padded query row whose visible keys all carry finfo.min (the usual
+    padding mask) gets the uniform average of those keys, as torch.softmax of
+    equal scores gives in the reference."""
+    g = torch.Generator().manual_seed(25)
+    q = torch.randn(1, 1, 6, 4, generator=g)
+    k = torch.randn(1, 1, 6, 4, generator=g)
+    v = torch.randn(1, 1, 6, 4, generator=g)
+    bias = torch.zeros(1, 1, 6, 6)
+    bias[:, :, :3, :] = torch.finfo(torch.float32).min   # rows 0..2: every key masked
+    o, _ = causal_attention(q, k, v, bias=bias)
+    for i in range(3):
+        assert torch.allclose(o[0, 0, i], v[0, 0, :i + 1].mean(0), atol=1e-6)
+
+
+def test_backward_with_bias_matches_fp64_autograd():
+    from oracle.attention import causal_attention_backward
+
+    g = torch.Generator().manual_seed(26)
+    q = torch.randn(2, 4, 7, 8, generator=g)
+    k = torch.randn(2, 2, 9, 8, generator=g)
+    v = torch.randn(2, 2, 9, 8, generator=g)
+    do = torch.randn(2, 4, 7, 8, generator=g)
+    bias = 1.5 * torch.randn(2, 1, 7, 9, generator=g)
+    bias[1, :, :, 0] = -1e4
+    got = causal_attention_backward(q, k, v, do, q_offset=2, bias=bias, row_chunk=3)
+    G = 2
+    qd, kd, vd = (t.double().clone().requires_grad_(True) for t in (q, k, v))
+    s = qd @ kd.repeat_interleave(G, 1).transpose(-1, -2) / math.sqrt(8) + bias.double()
+    mask = torch.arange(9).view(1, 9) > (torch.arange(7).view(7, 1) + 2)
+    o = torch.softmax(s.masked_fill(mask, float("-inf")), -1) @ vd.repeat_interleave(G, 1)
+    (o * do.double()).sum().backward()
+    for gt, rf in zip(got, (qd.grad, kd.grad, vd.grad)):
+        assert (gt.double() - rf).abs().max().item() < 1e-5

@@ -129,3 +129,39 @@ def test_paged_decode_ragged_and_empty():
         ob, lb = decode_attention(q[b:b + 1], kk, vv)
         assert torch.allclose(o[b], ob[0]) and torch.allclose(lse[b], lb[0])
     assert (o[2] == 0).all() and torch.isinf(lse[2]).all()
+
+
+def test_decode_bias_equals_last_prefill_row_with_the_same_mask():
+    """The decode oracle's additive mask matches the prefill oracle's on the last
+    query row (the reference adds attention_mask the same way on both paths,
+    models/llama3/attention.py:85-86)."""
+    from oracle.attention import causal_attention
+
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(2, 8, 1, 16, generator=g)
+    k = torch.randn(2, 2, 11, 16, generator=g)
+    v = torch.randn(2, 2, 11, 16, generator=g)
+    bias = 3.0 * torch.randn(2, 8, 11, generator=g)
+    bias[0, :, 4] = float("-inf")
+    o, lse = decode_attention(q, k, v, bias=bias)
+    op, lp = causal_attention(q, k, v, q_offset=10, bias=bias.unsqueeze(2))
+    assert torch.allclose(o, op, atol=1e-6) and torch.allclose(lse, lp[:, :, 0], atol=1e-6)
+
+
+def test_paged_bias_shorter_than_the_sequence_is_zero_past_its_end():
+    g = torch.Generator().manual_seed(32)
+    P, lens = 4, [9, 3]
+    kp = torch.randn(6, 1, P, 8, generator=g)
+    vp = torch.randn(6, 1, P, 8, generator=g)
+    bt = torch.tensor([[0, 2, 4], [1, -1, -1]], dtype=torch.int32)
+    q = torch.randn(2, 2, 1, 8, generator=g)
+    bias = torch.randn(2, 1, 5, generator=g)
+    o, lse = paged_decode(q, kp, vp, bt, torch.tensor(lens), bias=bias)
+    for b, L in enumerate(lens):
+        kk = gather_pages_torch(kp, bt[b:b + 1], L)
+        vv = gather_pages_torch(vp, bt[b:b + 1], L)
+        full = torch.zeros(1, 2, L)
+        n = min(L, 5)
+        full[..., :n] = bias[b:b + 1, :, :n]
+        r, rl = decode_attention(q[b:b + 1], kk, vv, bias=full)
+        assert torch.allclose(o[b:b + 1], r) and torch.allclose(lse[b:b + 1], rl)

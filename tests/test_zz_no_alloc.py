@@ -46,8 +46,8 @@ def _noalloc(lib, q, kp, vp, bt, sl, split, max_splits):
     rc = lib.lc_paged_decode_fwd_noalloc(
         q.data_ptr(), q.stride(0), q.stride(1), kp.data_ptr(), vp.data_ptr(), kp.stride(0),
         kp.stride(1), kp.stride(2), bt.data_ptr(), bt.stride(0), bt.shape[1], N, sl.data_ptr(),
-        out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr(), B, Hq, Hkv, D, P, split,
-        max_splits, 1.0 / math.sqrt(D), _native.lc_dtype(q),
+        out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr(), None, 0, 0, 0, 0, B, Hq,
+        Hkv, D, P, split, max_splits, 1.0 / math.sqrt(D), _native.lc_dtype(q),
         torch.cuda.current_stream().cuda_stream)
     _native.check(rc, "lc_paged_decode_fwd_noalloc")
     return out, lse
@@ -94,7 +94,7 @@ def test_noalloc_rejects_partials_beyond_the_scratch(cuda):
     lib = _native.load()
     assert lib.lc_paged_decode_workspace_bytes(64, 64, 128, 512) > 32 << 20
     rc = lib.lc_paged_decode_fwd_noalloc(
-        16, 128, 128, 16, 16, 1, 1, 1, 16, 512, 512, 1 << 20, 16, 16, 128, 128, None, 64, 64, 8,
-        128, 64, 64, 512, 1.0, 2, None)
+        16, 128, 128, 16, 16, 1, 1, 1, 16, 512, 512, 1 << 20, 16, 16, 128, 128, None, None, 0, 0,
+        0, 0, 64, 64, 8, 128, 64, 64, 512, 1.0, 2, None)
     assert rc == LC_EWORKSPACE
     assert b"scratch" in lib.lc_last_error()
