@@ -14,9 +14,10 @@ swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
 
 Prints one JSON line with the driver's fields plus `roofline` (the dominant
 kernel against MI355X peaks) and `cpu_baseline` (the CPU oracle on the host
-cores, bounded sample). The default run also measures the metric's other two
-figures, prefill TFLOP/s (config 3) and decode tok/s (config 4), and adds them
-under `secondary` (`--no-secondary` skips them).
+cores, bounded sample). The default run also measures the other BASELINE
+configs, prefill TFLOP/s (config 3), the 8B decode step's tok/s (config 4) and
+long-context decode GB/s (config 5), each with its own roofline and CPU
+baseline, under `secondary` (`--no-secondary` skips them).
 """
 from __future__ import annotations
 
@@ -486,7 +487,8 @@ def run_model(args):
                                                     "solutions" if args.tune_gemms else "")},
         "roofline": {"bound": "hbm", "kernel": "whole decode step (weights + KV read once)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("model8b_decode_step")},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _model_cpu_baseline(model, cfg, B, ctx)
@@ -694,8 +696,8 @@ def main() -> int:
     parser.add_argument("--prefill-shape", default=None, metavar="B,Hq,Hkv,S,D",
                         help="prefill: another shape instead of config 3 (4,32,8,4096,128)")
     parser.add_argument("--no-secondary", dest="secondary", action="store_false",
-                        help="decode8b: skip the prefill (config 3) and decode-step (config 4) "
-                             "figures added to the line under 'secondary'")
+                        help="decode8b: skip the config 3, 4 and 5 figures added to the line "
+                             "under 'secondary'")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
@@ -747,27 +749,31 @@ def main() -> int:
 
 
 def run_secondary(args) -> dict:
-    """The metric's other two figures, measured in the same run after the primary
-    one: prefill attention TFLOP/s at config 3 and decode tok/s at config 4 (same
-    steps and warm-up; no CPU baselines, which `--workload prefill` and
-    `--workload model8b` report). A failure is recorded, not raised, so the
-    primary line is still printed."""
+    """The BASELINE configs other than the headline one, measured in the same run
+    after it with the same steps and warm-up: prefill attention TFLOP/s at
+    config 3, the full 8B decode step's tok/s at config 4 and long-context paged
+    decode GB/s at config 5. Each entry carries its own `roofline` (with the
+    counter-measured traffic of its profiles/ summary) and, unless
+    --no-cpu-baseline, its bounded `cpu_baseline`. A failure is recorded, not
+    raised, so the primary line is still printed."""
     import copy
     import gc
 
     import torch
 
     sub = copy.copy(args)
-    sub.no_cpu_baseline = True
     sub.prefill_shape = None  # the secondary prefill figure is config 3
     out = {}
-    for key, fn in (("prefill_config3", run_prefill), ("decode_step_config4", run_model)):
+    jobs = (("prefill_config3", run_prefill), ("decode_step_config4", run_model),
+            ("decode70b_config5", lambda a: run_decode(a, decode70b_shape())))
+    for key, fn in jobs:
         try:
             r = fn(sub)
             out[key] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
-                        "workload": r["config"]["workload"],
-                        "frac_of_peak": r["roofline"]["frac"],
-                        "peak": f"{r['roofline']['peak']} {r['roofline']['unit']}"}
+                        "workload": r["config"]["workload"], "config": r["config"],
+                        "roofline": r["roofline"]}
+            if "cpu_baseline" in r:
+                out[key]["cpu_baseline"] = r["cpu_baseline"]
         except Exception as exc:  # recorded in the line
             out[key] = {"error": f"{type(exc).__name__}: {exc}"}
         gc.collect()
