@@ -441,17 +441,36 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
 # Paged decode  (reference: kernels/triton/decode_attention.py:204-287 over
 # models/llama3/kv_cache.py:65-83)
 # ---------------------------------------------------------------------------
-def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens: int) -> int:
+def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens: int,
+                        page_size: int = 64) -> int:
     """Tokens per split-K wave.
 
-    512-token splits measured fastest at both benchmark decode shapes (a split's
-    partial output costs 2 * G * D * 4 bytes of workspace traffic against
-    512 * D * 4 bytes of K/V, ~1.6% at G = 8); smaller splits are used only when
-    the grid would otherwise leave the 256 CUs idle.
+    Each split pays a fixed cost (its first dependent loads, its partial output
+    and its share of the merge) and a ragged batch ends in a tail of splits, so
+    the split size trades those against filling the 256 CUs. Measured on the
+    benchmark shapes (one wave per split, ~8 resident per CU):
+      * many (sequence, kv head) units (>= 256: config 2's 512, config 4's 256):
+        512-token splits; 256 was 3% slower at config 4 and larger splits lose
+        to the ragged tail at config 2;
+      * few units (config 5's 64 at 32K tokens): the largest of 2048 / 1024 /
+        512 that still gives >= 1024 splits (2048: 169 us against 186 us at 512);
+      * if even 512 leaves fewer than 1024 splits, halve down to 64.
+    Splits above 512 are used only where the row kernel (pages of a multiple
+    of 32 tokens, at most 64 pages per split) still takes them.
     """
-    split = 512
     units = batch * n_kv_heads * ((group + 15) // 16)
-    while split > 64 and units * ((capacity_tokens + split - 1) // split) < 2048:
+    rows_cap = 62 * page_size + 1 if page_size % 32 == 0 else 512
+
+    def n_splits(split: int) -> int:
+        return units * ((capacity_tokens + split - 1) // split)
+
+    split = 512
+    if units < 256:
+        for big in (2048, 1024):
+            if big <= rows_cap and n_splits(big) >= 1024:
+                split = big
+                break
+    while split > 64 and n_splits(split) < 1024:
         split //= 2
     return split
 
@@ -515,7 +534,7 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
     capacity = maxp * P
     G = Hq // Hkv
     if split_tokens is None:
-        split_tokens = choose_split_tokens(B, Hkv, G, capacity)
+        split_tokens = choose_split_tokens(B, Hkv, G, capacity, P)
     max_splits = max(1, (capacity + split_tokens - 1) // split_tokens)
     if scale is None:
         scale = 1.0 / math.sqrt(D)

@@ -185,14 +185,16 @@ def test_kv_cache_argument_checks():
 def test_split_heuristic():
     from llm_cuda.kernels._ops import choose_split_tokens
 
-    # both benchmark decode shapes use 512-token splits
+    # config 2 (64 ragged sequences) and config 4 (32 at 2K tokens): 512-token splits
     assert choose_split_tokens(64, 8, 4, 8192) == 512
-    assert choose_split_tokens(8, 8, 8, 32768) == 512
+    assert choose_split_tokens(32, 8, 4, 2112) == 512
+    # config 5 (8 sequences of 32K tokens, 64 units): 2048-token splits
+    assert choose_split_tokens(8, 8, 8, 32768) == 2048
     # tiny batch: splits shrink to keep the grid busy, never below 64.
     assert choose_split_tokens(1, 2, 4, 128) == 64
     for args in [(1, 1, 1, 1), (3, 5, 7, 1000), (64, 8, 16, 100000)]:
         s = choose_split_tokens(*args)
-        assert s % 64 == 0 and 64 <= s <= 1024
+        assert s % 64 == 0 and 64 <= s <= 2048
 
 
 def test_reference_attention_selectors_are_importable():
