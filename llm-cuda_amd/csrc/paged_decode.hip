@@ -235,10 +235,31 @@ __device__ __forceinline__ void store_partial(const DecodeArgs& a, int b, int h,
   if (q4 == 0) a.part_lse[pidx] = l_tot > 0.f ? m_ref + lc_log2(l_tot) : -INFINITY;
 }
 
-// Main kernel: page_size % 32 == 0 (every step inside one page). HB: the call
+// Query operands of head h (all zero for a padding head or past head_dim).
+template <typename T, int DPAD>
+__device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int h, bool head_ok, int q4,
+                                       typename MfmaOps<T>::v8 (&qop)[DPAD / 32]) {
+  typedef typename MfmaOps<T>::v8 v8;
+  const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+#pragma unroll
+  for (int s = 0; s < DPAD / 32; ++s) {
+    const int d0 = s * 32 + q4 * 8;
+    qop[s] = (head_ok && d0 < a.D) ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
+  }
+}
+
+// One wave's pass over tokens [t_begin, t_end) of (b, kvh) for its 16 query
+// heads, with page_size % 32 == 0 (every step inside one page), t_begin a
+// multiple of 32 and at most 64 pages touched (one block-table entry per
+// lane). Folds the range into the running state (o, m_ref, l_lane). lds_k and
+// lds_v are this wave's [32][DPAD + 16] tiles. load_q(qop) fills the query
+// operands; it runs after the block-table load is issued. HB: the call
 // carries an additive bias (loaded with the step's K/V, one step ahead).
-template <typename T, int DPAD, bool HB>
-__global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
+template <typename T, int DPAD, bool HB, typename QLoad>
+__device__ __forceinline__ void rows_range(const DecodeArgs& a, int b, int kvh, int h,
+                                           bool head_ok, int t_begin, int t_end, QLoad load_q,
+                                           T* lds_k, T* lds_v, f32x4_t (&o)[DPAD / 16],
+                                           float& m_ref, float& l_lane) {
   typedef MfmaOps<T> Ops;
   typedef typename Ops::v8 v8;
   constexpr int KS = DPAD / 32;      // MFMA k-steps over head_dim
@@ -247,48 +268,21 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   constexpr int RPI = 64 / CPR;      // token rows per load instruction
   constexpr int NI = kStep / RPI;    // load instructions per tensor per step
   constexpr int LROW = DPAD + 16;    // LDS row pitch (elements): rows 8 banks apart
-  __shared__ __align__(16) T lds_k[kStep * LROW];
-  __shared__ __align__(16) T lds_v[kStep * LROW];
 
-  const int lane = threadIdx.x;
-  const int split = blockIdx.z;
-  const int kvh = blockIdx.x / a.n_hgroups;
-  const int hg = blockIdx.x - kvh * a.n_hgroups;
-  const int b = blockIdx.y;
-  const int len = seq_len_of(a, b);
-  const int t_begin = split * a.split_tokens;
-  if (t_begin >= len) return;
-  const int t_end = min(len, t_begin + a.split_tokens);
-
+  const int lane = threadIdx.x & 63;
   const int col = lane & 15;  // query head within the 16-wide tile / token row of operands
   const int q4 = lane >> 4;   // 0..3
-  const int g = hg * 16 + col;
-  const bool head_ok = g < a.G;
-  const int h = kvh * a.G + g;
   const int srow = lane / CPR;    // staging: token row within a load instruction
   const int schunk = lane % CPR;  // staging: 16-byte chunk within the row
   const bool chunk_in_d = schunk * 8 < a.D;
 
-  // Block-table entries of this split, one per lane.
+  // Block-table entries of this range, one per lane.
   const int first_page = a.p_shift >= 0 ? (t_begin >> a.p_shift) : (t_begin / a.P);
   const int last_page = a.p_shift >= 0 ? ((t_end - 1) >> a.p_shift) : ((t_end - 1) / a.P);
   const int my_page =
       first_page + lane <= last_page ? a.bt[(int64_t)b * a.bt_stride + first_page + lane] : -1;
-
   v8 qop[KS];
-  {
-    const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int d0 = s * 32 + q4 * 8;
-      qop[s] = (head_ok && d0 < a.D) ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
-    }
-  }
-  f32x4_t o[DT];
-#pragma unroll
-  for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_ref = -INFINITY;
-  float l_lane = 0.f;
+  load_q(qop);
 
   u32x4_t sk[NI], sv[NI];
   // Bias of this lane's scores of the step at t: tokens t + gi*16 + q4*4 + i.
@@ -304,7 +298,7 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
         }
     }
   };
-  // Issue the loads of the step starting at t. Past the split end (the
+  // Issue the loads of the step starting at t. Past the range end (the
   // prefetch after the last step) every offset is out of range: zeros, no
   // memory traffic, and no branch for the wait-count bookkeeping to merge.
   auto issue = [&](int t) -> bool {
@@ -380,7 +374,152 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
     pv_step<T, DT, LROW>(lds_v, q4, col, pop, o);
     lc_compiler_fence();
   }
+}
+
+// Main kernel: page_size % 32 == 0; one wave per split, partials to the
+// workspace for the merge kernel.
+template <typename T, int DPAD, bool HB>
+__global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
+  typedef typename MfmaOps<T>::v8 v8;
+  constexpr int DT = DPAD / 16;
+  constexpr int LROW = DPAD + 16;
+  __shared__ __align__(16) T lds_k[kStep * LROW];
+  __shared__ __align__(16) T lds_v[kStep * LROW];
+
+  const int lane = threadIdx.x;
+  const int split = blockIdx.z;
+  const int kvh = blockIdx.x / a.n_hgroups;
+  const int hg = blockIdx.x - kvh * a.n_hgroups;
+  const int b = blockIdx.y;
+  const int len = seq_len_of(a, b);
+  const int t_begin = split * a.split_tokens;
+  if (t_begin >= len) return;
+  const int t_end = min(len, t_begin + a.split_tokens);
+
+  const int col = lane & 15;
+  const int q4 = lane >> 4;
+  const int g = hg * 16 + col;
+  const bool head_ok = g < a.G;
+  const int h = kvh * a.G + g;
+
+  f32x4_t o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -INFINITY;
+  float l_lane = 0.f;
+  rows_range<T, DPAD, HB>(
+      a, b, kvh, h, head_ok, t_begin, t_end,
+      [&](v8 (&qop)[DPAD / 32]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); }, lds_k, lds_v,
+      o, m_ref, l_lane);
   store_partial<DT>(a, b, h, split, head_ok, q4, m_ref, l_lane, o);
+}
+
+// Waves per workgroup of the single-split (cluster) kernel: its LDS is W
+// per-wave K/V tiles, kept within one CU's 160 KiB.
+template <int DPAD>
+constexpr int cluster_waves() {
+  return DPAD <= 128 ? 8 : 4;
+}
+
+// Single-split decode (max_splits == 1) for page_size % 32 == 0: one
+// workgroup of W waves per (b, kv head, group of <= 16 query heads). The
+// sequence's 32-token steps are dealt out evenly to the W waves by its
+// device-side length, each wave runs the main kernel's pass over its range,
+// and the W softmax states are merged through LDS into the final output and
+// lse, so no partials and no merge kernel:
+//   M = max_w m_w, out = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w,
+//   lse = (M + log2 sum_w 2^(m_w - M) l_w) * ln 2.
+// The host takes this path only when every wave's range touches <= 64 pages.
+template <typename T, int DPAD, bool HB>
+__global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_cluster_kernel(
+    DecodeArgs a, T* __restrict__ out, int64_t o_sb, int64_t o_sh, float* __restrict__ lse_out) {
+  typedef typename MfmaOps<T>::v8 v8;
+  constexpr int W = cluster_waves<DPAD>();
+  constexpr int DT = DPAD / 16;
+  constexpr int LROW = DPAD + 16;
+  constexpr int TILE = kStep * LROW;  // elements of one K or V tile
+  constexpr int OP = DPAD + 4;        // fp32 pitch of a head's row in the merge buffer
+  static_assert(16 * OP * 4 + 32 * 4 <= 2 * TILE * (int)sizeof(T),
+                "a wave's merge record must fit in its K/V tiles");
+  __shared__ __align__(16) T lds[W * 2 * TILE];
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int kvh = blockIdx.x / a.n_hgroups;
+  const int hg = blockIdx.x - kvh * a.n_hgroups;
+  const int b = blockIdx.y;
+  const int len = seq_len_of(a, b);
+  const int nsteps = (len + kStep - 1) / kStep;
+  const int t_begin = (wave * nsteps / W) * kStep;
+  const int t_end = min(len, ((wave + 1) * nsteps / W) * kStep);
+
+  const int col = lane & 15;
+  const int q4 = lane >> 4;
+  const int g = hg * 16 + col;
+  const bool head_ok = g < a.G;
+  const int h = kvh * a.G + g;
+
+  f32x4_t o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -INFINITY;
+  float l_lane = 0.f;
+  T* my_k = lds + wave * 2 * TILE;
+  T* my_v = my_k + TILE;
+  if (t_begin < t_end)
+    rows_range<T, DPAD, HB>(
+        a, b, kvh, h, head_ok, t_begin, t_end,
+        [&](v8 (&qop)[DPAD / 32]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); }, my_k, my_v,
+        o, m_ref, l_lane);
+
+  // This wave's record, over its own (now idle) tiles: o [16 heads][OP] fp32,
+  // then m [16] and l [16].
+  float l_tot = l_lane + __shfl_xor(l_lane, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  float* rec = reinterpret_cast<float*>(my_k);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    *reinterpret_cast<f32x4_t*>(rec + col * OP + dt * 16 + q4 * 4) = o[dt];
+  if (q4 == 0) {
+    rec[16 * OP + col] = m_ref;
+    rec[16 * OP + 16 + col] = l_tot;
+  }
+  __syncthreads();
+
+  // Combine: each thread owns 4 consecutive elements of one head's row.
+  constexpr int PER_HEAD = DPAD / 4;
+  for (int item = threadIdx.x; item < 16 * PER_HEAD; item += 64 * W) {
+    const int hc = item / PER_HEAD;
+    const int d0 = (item - hc * PER_HEAD) * 4;
+    const int gg = hg * 16 + hc;
+    if (gg >= a.G || d0 >= a.D) continue;
+    float mw[W], mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      mw[w] = reinterpret_cast<const float*>(lds + w * 2 * TILE)[16 * OP + hc];
+      mx = fmaxf(mx, mw[w]);
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, lsum = 0.f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float* r = reinterpret_cast<const float*>(lds + w * 2 * TILE);
+        const float e = mw[w] == -INFINITY ? 0.f : lc_exp2(mw[w] - mx);
+        lsum = fmaf(e, r[16 * OP + 16 + hc], lsum);
+        const f32x4_t ow = *reinterpret_cast<const f32x4_t*>(r + hc * OP + d0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(e, ow[i], acc[i]);
+      }
+    }
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    const int hh = kvh * a.G + gg;
+    T* oh = out + (int64_t)b * o_sb + (int64_t)hh * o_sh + d0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (d0 + i < a.D) oh[i] = lc_from_f32<T>(acc[i] * inv);
+    if (lse_out != nullptr && d0 == 0)
+      lse_out[(int64_t)b * a.Hq + hh] = lsum > 0.f ? (mx + lc_log2(lsum)) * kLn2 : -INFINITY;
+  }
 }
 
 // Page sizes that are not multiples of 32: per-lane page resolution.
@@ -635,10 +774,31 @@ int launch_merge(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, flo
   return lc_check_launch("lc_paged_decode_fwd (merge)");
 }
 
+template <typename T, int DPAD>
+int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, float* lse,
+                   hipStream_t st) {
+  dim3 grid(a.Hkv * a.n_hgroups, a.B);
+  const unsigned threads = 64 * cluster_waves<DPAD>();
+  T* o = static_cast<T*>(out);
+  if (a.bias != nullptr)
+    paged_decode_cluster_kernel<T, DPAD, true><<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse);
+  else
+    paged_decode_cluster_kernel<T, DPAD, false><<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse);
+  return lc_check_launch("lc_paged_decode_fwd (single split)");
+}
+
 template <typename T>
 int launch_decode(DecodeArgs a, void* out, int64_t o_sb, int64_t o_sh, float* lse, bool mfma,
-                  bool rows, hipStream_t st) {
+                  bool rows, bool cluster, hipStream_t st) {
   int rc = LC_OK;
+  if (mfma && cluster) {
+    if constexpr (sizeof(T) == 2) {
+      a.n_hgroups = (a.G + 15) / 16;
+      if (a.D <= 64) return launch_cluster<T, 64>(a, out, o_sb, o_sh, lse, st);
+      if (a.D <= 128) return launch_cluster<T, 128>(a, out, o_sb, o_sh, lse, st);
+      return launch_cluster<T, 256>(a, out, o_sb, o_sh, lse, st);
+    }
+  }
   if (mfma) {
     if constexpr (sizeof(T) == 2) {
       a.n_hgroups = (a.G + 15) / 16;
@@ -745,16 +905,24 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
   // most 64 pages (one per lane), and a page's head slice is addressable with
   // 31-bit byte offsets. A split that does not start on a page boundary
   // touches up to (split_tokens - 1) / page_size + 2 pages.
-  const bool rows = page_size % 32 == 0 && (split_tokens - 1) / page_size + 2 <= 64 &&
-                    ((page_size - 1) * kv_s_tok + D) * esz < (1LL << 31);
+  const bool row_pages = page_size % 32 == 0 &&
+                         ((page_size - 1) * kv_s_tok + D) * esz < (1LL << 31);
+  const bool rows = row_pages && (split_tokens - 1) / page_size + 2 <= 64;
+  // Single split (one workgroup of W waves per sequence and head group): every
+  // wave's share of the capacity, whole 32-token steps starting on a step
+  // boundary, must fit the row kernel's 64 block-table entries.
+  const int64_t waves = D <= 128 ? cluster_waves<128>() : cluster_waves<256>();
+  const int64_t cap_steps = (max_pages_per_seq * page_size + kStep - 1) / kStep;
+  const int64_t wave_tokens = (cap_steps + waves - 1) / waves * kStep;
+  const bool cluster = row_pages && max_splits == 1 && (wave_tokens - 1) / page_size + 2 <= 64;
   hipStream_t st = lc_stream(stream);
   switch (dtype) {
     case LC_DTYPE_F32:
-      return launch_decode<float>(a, out, o_sb, o_sh, lse, false, false, st);
+      return launch_decode<float>(a, out, o_sb, o_sh, lse, false, false, false, st);
     case LC_DTYPE_BF16:
-      return launch_decode<bf16_t>(a, out, o_sb, o_sh, lse, mfma, rows, st);
+      return launch_decode<bf16_t>(a, out, o_sb, o_sh, lse, mfma, rows, cluster, st);
     case LC_DTYPE_F16:
-      return launch_decode<f16_t>(a, out, o_sb, o_sh, lse, mfma, rows, st);
+      return launch_decode<f16_t>(a, out, o_sb, o_sh, lse, mfma, rows, cluster, st);
     default:
       return lc_fail(LC_EINVAL, "%s: unknown dtype %d", who, dtype);
   }

@@ -166,90 +166,99 @@ struct RopeAppendArgs {
   int Hq, Hkv, S, D;
 };
 
+// VEC consecutive elements of a row, held in registers.
 template <typename T, int VEC>
-__global__ __launch_bounds__(256) void rope_kv_append_kernel(KvPool pool, RopeAppendArgs a) {
+struct Chunk {
+  T v[VEC];
+};
+template <typename T, int VEC>
+__device__ __forceinline__ Chunk<T, VEC> chunk_load(const T* p) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    return __builtin_bit_cast(Chunk<T, VEC>, lc_load16(p));
+  } else {
+    Chunk<T, VEC> c;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) c.v[e] = p[e];
+    return c;
+  }
+}
+template <typename T, int VEC>
+__device__ __forceinline__ void chunk_store(T* p, const Chunk<T, VEC>& c) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    lc_store16(p, __builtin_bit_cast(Vec16<T>, c));
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) p[e] = c.v[e];
+  }
+}
+
+// One item per thread: a rotated chunk pair of a q or k row, or a copied chunk
+// of a v row. Every thread issues the same loads with no branch between them
+// (threads past the end repeat the last item, v items re-read their own chunk
+// and the first cos/sin chunk), so a pass costs two round trips before its
+// stores: the sources with seq_lens[b], then the cos/sin rows and the
+// block-table entry at position p.
+template <typename T, int VEC>
+__global__ __launch_bounds__(1024) void rope_kv_append_kernel(KvPool pool, RopeAppendArgs a) {
   const int b = blockIdx.x;
-  const int start = a.seq_lens[b];  // every thread reads it before the update below
   const int half = a.D / 2;
   const int hc = half / VEC;  // rotated chunk pairs per row
   const int vc = a.D / VEC;   // copied chunks per V row
   const int nq = a.S * a.Hq * hc;
   const int nk = a.S * a.Hkv * hc;
   const int nv = a.S * a.Hkv * vc;
+  const int total = nq + nk + nv;
+  const int capacity = pool.max_pages * pool.P;
   const T* cos = static_cast<const T*>(a.cos);
   const T* sin = static_cast<const T*>(a.sin);
-  for (int i = threadIdx.x; i < nq + nk + nv; i += blockDim.x) {
-    if (i < nq + nk) {
-      const bool isk = i >= nq;
-      const int j = isk ? i - nq : i;
-      const int heads = isk ? a.Hkv : a.Hq;
-      const int c = j % hc;
-      const int hs = j / hc;
-      const int h = hs % heads;
-      const int s = hs / heads;
-      const int pos = start + s;
-      const int prow = pos < 0 ? 0 : (pos >= a.table_rows ? a.table_rows - 1 : pos);
-      const int d0 = c * VEC;
-      const T* src = isk ? static_cast<const T*>(a.k) + b * a.ks[0] + h * a.ks[1] + s * a.ks[2]
-                         : static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1] + s * a.qs[2];
-      const T* cp = cos + (int64_t)prow * a.cs;
-      const T* sp = sin + (int64_t)prow * a.ss;
-      T* dst;
-      if (isk) {
-        const int64_t off = pool_offset(pool, b, h, pos);
-        if (off < 0) continue;
-        dst = static_cast<T*>(pool.kp) + off;
-      } else {
-        dst = static_cast<T*>(a.qo) + b * a.qos[0] + h * a.qos[1] + s * a.qos[2];
-      }
-      float x1[VEC], x2[VEC], c1[VEC], c2[VEC], s1[VEC], s2[VEC];
-      if constexpr (VEC * sizeof(T) == 16) {
-        const Vec16<T> va = lc_load16(src + d0), vb = lc_load16(src + d0 + half);
-        const Vec16<T> ca = lc_load16(cp + d0), cb = lc_load16(cp + d0 + half);
-        const Vec16<T> sa = lc_load16(sp + d0), sb = lc_load16(sp + d0 + half);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          x1[e] = lc_to_f32(va.v[e]);
-          x2[e] = lc_to_f32(vb.v[e]);
-          c1[e] = lc_to_f32(ca.v[e]);
-          c2[e] = lc_to_f32(cb.v[e]);
-          s1[e] = lc_to_f32(sa.v[e]);
-          s2[e] = lc_to_f32(sb.v[e]);
-        }
-        Vec16<T> o1, o2;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          o1.v[e] = lc_from_f32<T>(x1[e] * c1[e] - x2[e] * s1[e]);
-          o2.v[e] = lc_from_f32<T>(x2[e] * c2[e] + x1[e] * s2[e]);
-        }
-        lc_store16(dst + d0, o1);
-        lc_store16(dst + d0 + half, o2);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float u1 = lc_to_f32(src[d0 + e]), u2 = lc_to_f32(src[d0 + e + half]);
-          dst[d0 + e] = lc_from_f32<T>(u1 * lc_to_f32(cp[d0 + e]) - u2 * lc_to_f32(sp[d0 + e]));
-          dst[d0 + e + half] =
-              lc_from_f32<T>(u2 * lc_to_f32(cp[d0 + e + half]) + u1 * lc_to_f32(sp[d0 + e + half]));
-        }
-      }
-    } else {
-      const int j = i - nq - nk;
-      const int c = j % vc;
-      const int hs = j / vc;
-      const int h = hs % a.Hkv;
-      const int s = hs / a.Hkv;
-      const int64_t off = pool_offset(pool, b, h, start + s);
-      if (off < 0) continue;
-      const T* src = static_cast<const T*>(a.v) + b * a.vs[0] + h * a.vs[1] + s * a.vs[2] + c * VEC;
-      T* dst = static_cast<T*>(pool.vp) + off + c * VEC;
-      if constexpr (VEC * sizeof(T) == 16) {
-        lc_store16(dst, lc_load16(src));
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) dst[e] = src[e];
-      }
+  const int start = a.seq_lens[b];  // every thread reads it before the update below
+  for (int i0 = 0; i0 < total; i0 += blockDim.x) {
+    const int i = i0 + threadIdx.x;
+    const int ic = i < total ? i : total - 1;
+    const int kind = ic < nq ? 0 : (ic < nq + nk ? 1 : 2);  // q, k, v
+    const int j = kind == 0 ? ic : (kind == 1 ? ic - nq : ic - nq - nk);
+    const int per_row = kind == 2 ? vc : hc;
+    const int heads = kind == 0 ? a.Hq : a.Hkv;
+    const int c = j % per_row;
+    const int hs = j / per_row;
+    const int h = hs % heads;
+    const int s = hs / heads;
+    const int d0 = c * VEC;
+    const T* src = kind == 0 ? static_cast<const T*>(a.q) + b * a.qs[0] + h * a.qs[1] + s * a.qs[2]
+                 : kind == 1 ? static_cast<const T*>(a.k) + b * a.ks[0] + h * a.ks[1] + s * a.ks[2]
+                             : static_cast<const T*>(a.v) + b * a.vs[0] + h * a.vs[1] + s * a.vs[2];
+    const Chunk<T, VEC> xa = chunk_load<T, VEC>(src + d0);
+    const Chunk<T, VEC> xb = chunk_load<T, VEC>(src + (kind == 2 ? d0 : d0 + half));
+    const int pos = start + s;
+    const int prow = pos < 0 ? 0 : (pos >= a.table_rows ? a.table_rows - 1 : pos);
+    const int dc = kind == 2 ? 0 : d0;
+    const T* cp = cos + (int64_t)prow * a.cs + dc;
+    const T* sp = sin + (int64_t)prow * a.ss + dc;
+    const Chunk<T, VEC> ca = chunk_load<T, VEC>(cp), cb = chunk_load<T, VEC>(cp + half);
+    const Chunk<T, VEC> sa = chunk_load<T, VEC>(sp), sb = chunk_load<T, VEC>(sp + half);
+    const bool in_cap = pos >= 0 && pos < capacity;
+    const int page_idx = in_cap ? pos / pool.P : 0;
+    const int phys = pool.bt[(int64_t)b * pool.bt_stride + page_idx];
+    // A k/v item whose position has no valid page is dropped.
+    const bool paged_ok = in_cap && static_cast<unsigned>(phys) < static_cast<unsigned>(pool.num_pages);
+    if (!((i < total) & ((kind == 0) | paged_ok))) continue;
+    const int64_t off = (int64_t)phys * pool.s_page + (int64_t)h * pool.s_head +
+                        (int64_t)(pos - page_idx * pool.P) * pool.s_tok;
+    if (kind == 2) {
+      chunk_store<T, VEC>(static_cast<T*>(pool.vp) + off + d0, xa);
+      continue;
     }
+    Chunk<T, VEC> o1, o2;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float x1 = lc_to_f32(xa.v[e]), x2 = lc_to_f32(xb.v[e]);
+      o1.v[e] = lc_from_f32<T>(x1 * lc_to_f32(ca.v[e]) - x2 * lc_to_f32(sa.v[e]));
+      o2.v[e] = lc_from_f32<T>(x2 * lc_to_f32(cb.v[e]) + x1 * lc_to_f32(sb.v[e]));
+    }
+    T* dst = kind == 1 ? static_cast<T*>(pool.kp) + off
+                       : static_cast<T*>(a.qo) + b * a.qos[0] + h * a.qos[1] + s * a.qos[2];
+    chunk_store<T, VEC>(dst + d0, o1);
+    chunk_store<T, VEC>(dst + d0 + half, o2);
   }
   __syncthreads();
   if (threadIdx.x == 0) a.seq_lens[b] = start + a.S;
@@ -266,10 +275,16 @@ int launch_rope_append(const KvPool& pool, const RopeAppendArgs& a, int64_t B, h
   for (int i = 0; i < 3; ++i)
     vec_ok = vec_ok && a.qs[i] % V == 0 && a.ks[i] % V == 0 && a.vs[i] % V == 0 &&
              a.qos[i] % V == 0;
+  // Items per sequence: (Hq + Hkv) rotated rows of D/2/vec chunk pairs and
+  // Hkv copied rows of D/vec chunks per new token; one thread each, up to 1024.
+  const int64_t hc = a.D / 2 / (vec_ok ? V : 1);
+  const int64_t items = (int64_t)a.S * (a.Hq + 3 * a.Hkv) * hc;
+  const unsigned threads = (unsigned)(items >= 1024 ? 1024 : lc_cdiv(items, 64) * 64);
+  if (threads == 0) return LC_OK;
   if (vec_ok)
-    rope_kv_append_kernel<T, V><<<(unsigned)B, 256, 0, st>>>(pool, a);
+    rope_kv_append_kernel<T, V><<<(unsigned)B, threads, 0, st>>>(pool, a);
   else
-    rope_kv_append_kernel<T, 1><<<(unsigned)B, 256, 0, st>>>(pool, a);
+    rope_kv_append_kernel<T, 1><<<(unsigned)B, threads, 0, st>>>(pool, a);
   return lc_check_launch("lc_rope_kv_append");
 }
 

@@ -24,6 +24,18 @@ def _stream(dev: torch.device) -> int:
     return nat.stream_ptr(dev)
 
 
+_CU_COUNTS: dict[int, int] = {}
+
+
+def _cu_count(dev: torch.device) -> int:
+    """Compute units of the device (cached per device index)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    n = _CU_COUNTS.get(idx)
+    if n is None:
+        n = _CU_COUNTS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return n
+
+
 class _DeviceGuard:
     """Make `dev` current for the launch if it is not already."""
 
@@ -441,9 +453,31 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
 # Paged decode  (reference: kernels/triton/decode_attention.py:204-287 over
 # models/llama3/kv_cache.py:65-83)
 # ---------------------------------------------------------------------------
+def single_split_fits(capacity_tokens: int, page_size: int, head_dim: int) -> bool:
+    """Whether one split covering the capacity runs the single-split kernel
+    (one workgroup of 8 waves, 4 above head_dim 128, per sequence and head
+    group): pages of a multiple of 32 tokens, and every wave's share of the
+    capacity's 32-token steps within 64 pages."""
+    if page_size % 32 != 0:
+        return False
+    waves = 8 if head_dim <= 128 else 4
+    steps = -(-capacity_tokens // 32)
+    wave_tokens = -(-steps // waves) * 32
+    return (wave_tokens - 1) // page_size + 2 <= 64
+
+
 def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens: int,
-                        page_size: int = 64) -> int:
+                        page_size: int = 64, head_dim: int = 128,
+                        uniform_lengths: bool = False, n_cus: int = 256) -> int:
     """Tokens per split-K wave.
+
+    With uniform_lengths (every sequence of the batch equally long, as in a
+    batched decode step) and units filling whole rounds of the CUs, one split
+    covers the capacity: the single-split kernel gives each unit one
+    workgroup whose waves share its tokens evenly and merge in LDS, with no
+    partials and no merge kernel (config 4: 43.6 us against 46.0 us for
+    512-token splits; 82.7 against 85.3 at 4096 tokens). It is kept off
+    ragged batches, where the longest sequence would set every unit's time.
 
     Each split pays a fixed cost (its first dependent loads, its partial output
     and its share of the merge) and a ragged batch ends in a tail of splits, so
@@ -459,6 +493,9 @@ def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens
     of 32 tokens, at most 64 pages per split) still takes them.
     """
     units = batch * n_kv_heads * ((group + 15) // 16)
+    if (uniform_lengths and units >= n_cus and units % n_cus == 0
+            and single_split_fits(capacity_tokens, page_size, head_dim)):
+        return -(-capacity_tokens // 64) * 64
     rows_cap = 62 * page_size + 1 if page_size % 32 == 0 else 512
 
     def n_splits(split: int) -> int:
@@ -479,16 +516,19 @@ def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Te
                  block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None = None,
                  return_lse: bool = False, split_tokens: int | None = None,
                  workspace: torch.Tensor | None = None,
-                 attention_mask: torch.Tensor | None = None):
+                 attention_mask: torch.Tensor | None = None, uniform_lengths: bool = False):
     """One-token GQA attention per sequence over a paged K/V pool (forward only).
 
     q: [B, Hq, 1, D] or [B, Hq, D]; key_pages, value_pages: [N, Hkv, P, D];
     block_table: int32 [B, max_pages]; seq_lens: int32 [B]. attention_mask:
     additive scores for the query token, broadcastable to [B, Hq, 1, L] (or
     [B, Hq, L]); token t < L of a sequence gets mask[..., t], later tokens
-    none. Returns out with q's shape (and lse [B, Hq] fp32 if return_lse).
+    none. uniform_lengths: the caller knows every seq_lens entry is equal (a
+    hint for the split choice only; results do not depend on it). Returns out
+    with q's shape (and lse [B, Hq] fp32 if return_lse).
     """
-    args = (block_table, seq_lens, scale, return_lse, split_tokens, workspace, attention_mask)
+    args = (block_table, seq_lens, scale, return_lse, split_tokens, workspace, attention_mask,
+            uniform_lengths)
     if _records_grad(q, key_pages, value_pages):
         return _ForwardOnly.apply("paged_decode", lambda a, k, v: _paged_decode(a, k, v, *args),
                                   q, key_pages, value_pages)
@@ -498,7 +538,7 @@ def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Te
 def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
                   block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None,
                   return_lse: bool, split_tokens: int | None, workspace: torch.Tensor | None,
-                  attention_mask: torch.Tensor | None = None):
+                  attention_mask: torch.Tensor | None = None, uniform_lengths: bool = False):
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
     if q4.dim() != 4 or q4.shape[2] != 1:
@@ -534,7 +574,8 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
     capacity = maxp * P
     G = Hq // Hkv
     if split_tokens is None:
-        split_tokens = choose_split_tokens(B, Hkv, G, capacity, P)
+        split_tokens = choose_split_tokens(B, Hkv, G, capacity, P, D, uniform_lengths,
+                                           _cu_count(dev))
     max_splits = max(1, (capacity + split_tokens - 1) // split_tokens)
     if scale is None:
         scale = 1.0 / math.sqrt(D)

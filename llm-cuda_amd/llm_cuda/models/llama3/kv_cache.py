@@ -90,6 +90,11 @@ class PagedKVLayerCache:
             raise ValueError("sequences have different lengths; use `lengths`")
         return first
 
+    @property
+    def uniform_lengths(self) -> bool:
+        """Whether every sequence holds the same number of tokens (host mirror)."""
+        return all(n == self.lengths[0] for n in self.lengths)
+
     def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
         if k.shape != v.shape:
             raise ValueError("k and v shapes must match")

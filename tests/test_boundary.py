@@ -195,6 +195,33 @@ def test_split_heuristic():
     for args in [(1, 1, 1, 1), (3, 5, 7, 1000), (64, 8, 16, 100000)]:
         s = choose_split_tokens(*args)
         assert s % 64 == 0 and 64 <= s <= 2048
+    # uniform lengths with whole rounds of 256 units: one split over the capacity
+    assert choose_split_tokens(32, 8, 4, 2112, 64, 128, True) == 2112
+    assert choose_split_tokens(64, 8, 4, 4160, 64, 128, True) == 4160
+    assert choose_split_tokens(32, 8, 4, 2100, 64, 128, True) == 2112  # rounded up to 64
+    # ... but not for 384 units (1.5 rounds), 128 units, pages of 48 tokens, or
+    # a capacity whose per-wave share exceeds 64 pages (8 waves x 62 pages)
+    assert choose_split_tokens(48, 8, 4, 2112, 64, 128, True) == 512
+    assert choose_split_tokens(16, 8, 4, 2112, 64, 128, True) < 2112
+    assert choose_split_tokens(32, 8, 4, 2112, 48, 128, True) == 512
+    assert choose_split_tokens(32, 8, 4, 40000, 64, 128, True) == 512
+    # head_dim 256 runs 4 waves per workgroup: half the capacity fits
+    assert choose_split_tokens(32, 8, 4, 16384, 64, 128, True) == 16384
+    assert choose_split_tokens(32, 8, 4, 16384, 64, 256, True) == 512
+
+
+def test_single_split_fit_matches_the_library_rule():
+    """single_split_fits mirrors the C dispatch rule: 8 waves up to head_dim
+    128 (4 above), each wave's whole 32-token steps within 64 pages."""
+    from llm_cuda.kernels._ops import single_split_fits
+
+    # a wave's range starts on a 32-token step, so 4032 tokens (126 steps)
+    # touch at most 64 pages of 64: 8 x 4032 = 32256 tokens is the largest
+    # capacity, 4 x 4032 = 16128 at head_dim 256
+    assert single_split_fits(32256, 64, 128)
+    assert not single_split_fits(32257, 64, 128)
+    assert single_split_fits(16128, 64, 256) and not single_split_fits(16129, 64, 256)
+    assert not single_split_fits(1024, 48, 128)
 
 
 def test_reference_attention_selectors_are_importable():

@@ -257,3 +257,53 @@ def test_paged_lanes_kernel_small_head_dim(cuda, dtype, D, P):
     ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
     assert_close(out, ref, ATOL[dtype], f"lanes D={D} P={P}")
     assert_lse_close(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Hq,Hkv,D,P", [(32, 8, 128, 64), (16, 4, 64, 32), (8, 2, 256, 128),
+                                        (40, 2, 48, 64), (8, 1, 128, 96)])
+def test_single_split_workgroup_kernel(cuda, dtype, Hq, Hkv, D, P):
+    """One split covering the capacity (max_splits == 1) runs one workgroup of
+    several waves per (sequence, group of <= 16 query heads): the steps are
+    dealt out to the waves by the device-side length and the waves' softmax
+    states merge in LDS, with no merge kernel. Lengths 0, 1, fewer steps than
+    waves, one token past a step, ragged, and a full 2049-token context; G = 20
+    spans two head groups; head_dim 48 is padded to 64."""
+    lens = [0, 1, 31, 33, 257, 1000, 2049]
+    q, kp, vp, bt, sl = _paged_case(lens, Hq, Hkv, D, P, dtype, cuda, seed=Hq + D + P)
+    split = -(-bt.shape[1] * P // 64) * 64
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda, split_tokens=split)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert (out[0].float().cpu() == 0).all() and torch.isinf(lse[0].cpu()).all()
+    assert_close(out[1:], ref[1:], ATOL[dtype], f"single split Hq={Hq} D={D} P={P}")
+    assert_lse_close(lse[1:], ref_lse[1:])
+    # the split-K path on the same inputs agrees to fp32 rounding of the merge
+    out2, lse2 = _run_paged(q, kp, vp, bt, sl, cuda, split_tokens=256)
+    assert_close(out, out2, ATOL[dtype], "single split vs split-K")
+    assert_lse_close(lse, lse2)
+
+
+def test_single_split_invalid_entry_and_clamped_length(cuda):
+    """Single-split kernel: a bad page id inside the live range drops that
+    page's tokens, and lengths beyond the table capacity are clamped to it."""
+    lens = [192, 100]
+    q, kp, vp, bt, sl = _paged_case(lens, 16, 2, 128, 64, torch.bfloat16, cuda, seed=41,
+                                    poison=False)
+    good = bt.clone()
+    bt[0, 1] = -5
+    sl_run = torch.tensor([192, 10 ** 6], dtype=torch.int32)  # 1e6 clamps to 192
+    out, lse = _run_paged(q, kp, vp, bt, sl_run, cuda, split_tokens=192)
+    keep = [0, 2]
+    kk = torch.cat([kp[int(good[0, i])] for i in keep], dim=1)[None]
+    vv = torch.cat([vp[int(good[0, i])] for i in keep], dim=1)[None]
+    ref0, ref0_lse = decode_attention(q[:1], kk, vv)
+    assert_close(out[:1], ref0, ATOL[torch.bfloat16], "single split, invalid page")
+    assert_lse_close(lse[:1], ref0_lse)
+    # sequence 1 owns two pages; its third entry is -1, so of the clamped 192
+    # tokens the first 128 remain
+    kk = torch.cat([kp[int(bt[1, i])] for i in (0, 1)], dim=1)[None]
+    vv = torch.cat([vp[int(bt[1, i])] for i in (0, 1)], dim=1)[None]
+    ref1, ref1_lse = decode_attention(q[1:], kk, vv)
+    assert_close(out[1:], ref1, ATOL[torch.bfloat16], "single split, clamped length")
+    assert_lse_close(lse[1:], ref1_lse)
+

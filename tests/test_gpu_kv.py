@@ -85,17 +85,19 @@ def test_append_drops_tokens_beyond_capacity_or_bad_pages(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("S,D", [(1, 64), (3, 128), (2, 20)])
-def test_rope_kv_append_equals_rope_then_append(cuda, dtype, S, D):
+@pytest.mark.parametrize("S,D,Hq,Hkv", [(1, 64, 4, 2), (3, 128, 4, 2), (2, 20, 4, 2),
+                                         (5, 128, 32, 8)])
+def test_rope_kv_append_equals_rope_then_append(cuda, dtype, S, D, Hq, Hkv):
     """The fused decode-time op equals the RoPE kernel followed by the page
     append and the length update, bit for bit: rotated q, both pools (with a
     ragged batch, an invalid page entry and strided projection views) and the
-    advanced seq_lens. D = 20 takes the element-wise path."""
+    advanced seq_lens. D = 20 takes the element-wise path; the 32/8-head case
+    has more items per sequence than one workgroup's 1024 threads."""
     from llm_cuda.kernels import _ops
     from llm_cuda.models.llama3.rotary import build_rope_cache
 
-    g = torch.Generator().manual_seed(S * 100 + D)
-    B, Hq, Hkv, P, maxp = 3, 4, 2, 8, 5
+    g = torch.Generator().manual_seed(S * 100 + D + Hq)
+    B, P, maxp = 3, 8, 5
     N = B * maxp + 1
     table = torch.randperm(N, generator=g)[: B * maxp].to(torch.int32).view(B, maxp)
     table[2, 3] = -1  # sequence 2: its 4th page is unmapped (tokens dropped)

@@ -165,11 +165,13 @@ def _paged(lens, Hq, Hkv, D, P, dtype, seed):
 @pytest.mark.parametrize("dtype,P", [(torch.bfloat16, 64), (torch.bfloat16, 48),
                                      (torch.float16, 64), (torch.float32, 64)])
 @pytest.mark.parametrize("per_head", [False, True])
-def test_paged_decode_masks(cuda, dtype, P, per_head):
+@pytest.mark.parametrize("single_split", [False, True])
+def test_paged_decode_masks(cuda, dtype, P, per_head, single_split):
     """Rows kernel (P 64), per-lane-page kernel (P 48), generic kernel (fp32);
-    a [B, 1, 1, L] key mask or a [B, Hq, 1, L] per-head mask, with -inf, -1e4
-    and random entries, shorter than the longest sequence (later tokens get no
-    mask)."""
+    with single_split, one split covers the capacity (the multi-wave
+    workgroup kernel at P 64); a [B, 1, 1, L] key mask or a [B, Hq, 1, L]
+    per-head mask, with -inf, -1e4 and random entries, shorter than the
+    longest sequence (later tokens get no mask)."""
     from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
 
     lens = [700, 1, 64, 1300]
@@ -180,8 +182,10 @@ def test_paged_decode_masks(cuda, dtype, P, per_head):
     mask[0, ..., 100:200] = float("-inf")
     mask[3, ..., :50] = -1e4
     mask = mask.to(dtype if dtype != torch.float16 else torch.float32)
+    split = -(-bt.shape[1] * P // 64) * 64 if single_split else None
     out, lse = paged_decode_attention(q.to(cuda), kp.to(cuda), vp.to(cuda), bt.to(cuda),
-                                      sl.to(cuda), return_lse=True, attention_mask=mask.to(cuda))
+                                      sl.to(cuda), return_lse=True, attention_mask=mask.to(cuda),
+                                      split_tokens=split)
     ref, ref_lse = paged_decode(q, kp, vp, bt, sl, bias=mask[:, :, 0])
     assert_close(out, ref, ATOL[dtype], "decode mask")
     assert_lse_close(lse, ref_lse)
