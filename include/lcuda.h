@@ -205,6 +205,12 @@ LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D,
  * split_tokens: tokens per split (multiple of 64); max_splits *
  *   split_tokens must cover the block-table capacity max_pages_per_seq *
  *   page_size (so no clamped length can need more splits than the grid has).
+ *   max_splits == 1 (bf16/f16, page_size a multiple of 32, a capacity within
+ *   the limit of lc_paged_decode_step) runs one workgroup of 8 waves (4 above
+ *   head_dim 128) per (sequence, head group) that shares the sequence's
+ *   tokens evenly among its waves and merges them in LDS, with no merge
+ *   launch; it suits batches of equal lengths whose units (sequences x kv
+ *   heads x head groups) fill whole rounds of the CUs.
  * workspace: >= lc_paged_decode_workspace_bytes(B, Hq, D, max_splits). */
 LC_API int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* key_pages,
                         const void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
@@ -284,6 +290,49 @@ LC_API int lc_rope_kv_append(const void* q, const int64_t* q_strides, const void
                       int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
                       int32_t* seq_lens, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                       int64_t page_size, int dtype, void* stream);
+
+/* One decode step of attention in one launch: lc_rope_kv_append with S = 1
+ * followed by lc_paged_decode_fwd over the advanced lengths, without the
+ * rotated q ever leaving the kernel. With p = seq_lens[b] (read before the
+ * update):
+ *   key_pages/value_pages at slot p   <- rope(k[b, h], p), v[b, h]
+ *   out[b, h, :] = softmax(rope(q[b, h], p) . K_b^T * scale [+ bias]) V_b
+ *                  over tokens 0 .. min(p + 1, capacity) - 1 of sequence b
+ *   seq_lens[b] = p + 1
+ * with the conventions of those two entries (tokens with invalid page entries
+ * are dropped, lengths clamp to the capacity max_pages_per_seq * page_size,
+ * lse (may be NULL) natural-log, bias as in lc_paged_decode_fwd over token
+ * indices including p). rope() is rounded to dtype before use, so results
+ * equal the two-launch sequence up to fp32 summation order. Runs the
+ * single-split kernel: one workgroup of 8 waves (4 above head_dim 128) per
+ * (sequence, group of <= 16 query heads), the cached tokens dealt out evenly
+ * to its waves. Replaces the decode branch of models/llama3/attention.py:
+ * 100-150 (RoPE at past_len, kv_cache.py:38-63 append, then the decode
+ * attention of kernels/triton/decode_attention.py:204-287 over the
+ * kv_cache.py:65-83 copy).
+ * q: [B, Hq, D], k, v: [B, Hkv, D] (strides q_sb/q_sh, k_sb/k_sh, v_sb/v_sh;
+ *   head_dim contiguous); out: [B, Hq, D] with strides o_sb/o_sh.
+ * counters: int32 [B] device scratch that must hold zeros; each launch leaves
+ *   it at zero (the last workgroup of a sequence to finish advances its
+ *   length). Launches that share counters or seq_lens must not overlap.
+ * Requires dtype bf16 or f16, head_dim a multiple of 16 (<= 256), page_size a
+ * multiple of 32, a capacity of at most 126 steps of 32 tokens per wave
+ * (32256 tokens at head_dim <= 128, 16128 above, for page_size 64), cos/sin
+ * tables covering the capacity, 16-byte-aligned q, cos, sin and pools with
+ * strides in multiples of 8 elements, and 8-byte-aligned k, v with strides in
+ * multiples of 4; otherwise LC_EINVAL without a launch. */
+LC_API int lc_paged_decode_step(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
+                                int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb,
+                                int64_t v_sh, const void* cos, const void* sin,
+                                int64_t cos_stride, int64_t sin_stride, int64_t table_rows,
+                                void* key_pages, void* value_pages, int64_t kv_s_page,
+                                int64_t kv_s_head, int64_t kv_s_tok, const int32_t* block_table,
+                                int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
+                                int32_t* seq_lens, int32_t* counters, void* out, int64_t o_sb,
+                                int64_t o_sh, float* lse, const void* bias, int64_t bias_sb,
+                                int64_t bias_sh, int64_t bias_len, int bias_dtype, int64_t B,
+                                int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                                float scale, int dtype, void* stream);
 
 /* Gather the first L tokens of every sequence into contiguous
  * k_out, v_out [B, Hkv, L, D] (bit-exact copy through the block table).

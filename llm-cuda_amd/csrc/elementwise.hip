@@ -354,8 +354,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor t1, RopeTensor t2,
   Vec16<T> o1, o2;
 #pragma unroll
   for (int e = 0; e < VEC; ++e) {
-    const T lo = lc_from_f32<T>(x1[e] * c1[e] - x2[e] * s1[e]);
-    const T hi = lc_from_f32<T>(x2[e] * c2[e] + x1[e] * s2[e]);
+    const T lo = lc_from_f32<T>(lc_rope_lo(x1[e], x2[e], c1[e], s1[e]));
+    const T hi = lc_from_f32<T>(lc_rope_hi(x1[e], x2[e], c2[e], s2[e]));
     if constexpr (VEC * sizeof(T) == 16) {
       o1.v[e] = lo;
       o2.v[e] = hi;

@@ -87,6 +87,16 @@ __device__ __forceinline__ void lc_store16_nt(T* p, const Vec16<T>& x) {
 __device__ __forceinline__ float lc_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float lc_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// RoPE of one element pair (x1 at d, x2 at d + D/2) with full-width tables,
+// in fp32 with one fixed rounding order shared by every kernel that rotates:
+//   lo = x1 c1 - x2 s1 (tables at d),  hi = x2 c2 + x1 s2 (tables at d + D/2).
+__device__ __forceinline__ float lc_rope_lo(float x1, float x2, float c1, float s1) {
+  return fmaf(x1, c1, -(x2 * s1));
+}
+__device__ __forceinline__ float lc_rope_hi(float x1, float x2, float c2, float s2) {
+  return fmaf(x2, c2, x1 * s2);
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 

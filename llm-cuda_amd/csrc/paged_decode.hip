@@ -252,14 +252,17 @@ __device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int h, bool h
 // heads, with page_size % 32 == 0 (every step inside one page), t_begin a
 // multiple of 32 and at most 64 pages touched (one block-table entry per
 // lane). Folds the range into the running state (o, m_ref, l_lane). lds_k and
-// lds_v are this wave's [32][DPAD + 16] tiles. load_q(qop) fills the query
-// operands; it runs after the block-table load is issued. HB: the call
-// carries an additive bias (loaded with the step's K/V, one step ahead).
-template <typename T, int DPAD, bool HB, typename QLoad>
+// lds_v are this wave's [32][DPAD + 16] tiles. load_q(qop) issues the query
+// operand loads after the block-table load; finish_q(qop) runs after the
+// first step's K/V loads are issued (a place for arithmetic on the loaded
+// operands that should not hold up that issue). HB: the call carries an
+// additive bias (loaded with the step's K/V, one step ahead).
+template <typename T, int DPAD, bool HB, typename QLoad, typename QFinish>
 __device__ __forceinline__ void rows_range(const DecodeArgs& a, int b, int kvh, int h,
                                            bool head_ok, int t_begin, int t_end, QLoad load_q,
-                                           T* lds_k, T* lds_v, f32x4_t (&o)[DPAD / 16],
-                                           float& m_ref, float& l_lane) {
+                                           QFinish finish_q, T* lds_k, T* lds_v,
+                                           f32x4_t (&o)[DPAD / 16], float& m_ref,
+                                           float& l_lane) {
   typedef MfmaOps<T> Ops;
   typedef typename Ops::v8 v8;
   constexpr int KS = DPAD / 32;      // MFMA k-steps over head_dim
@@ -330,6 +333,7 @@ __device__ __forceinline__ void rows_range(const DecodeArgs& a, int b, int kvh, 
 
   bool pvalid = issue(t_begin);
   issue_bias(t_begin);
+  finish_q(qop);
   for (int t = t_begin; t < t_end; t += kStep) {
     // staging -> LDS (row-major [32 tok][LROW])
 #pragma unroll
@@ -409,8 +413,8 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   float l_lane = 0.f;
   rows_range<T, DPAD, HB>(
       a, b, kvh, h, head_ok, t_begin, t_end,
-      [&](v8 (&qop)[DPAD / 32]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); }, lds_k, lds_v,
-      o, m_ref, l_lane);
+      [&](v8 (&qop)[DPAD / 32]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); },
+      [](v8 (&)[DPAD / 32]) {}, lds_k, lds_v, o, m_ref, l_lane);
   store_partial<DT>(a, b, h, split, head_ok, q4, m_ref, l_lane, o);
 }
 
@@ -421,6 +425,23 @@ constexpr int cluster_waves() {
   return DPAD <= 128 ? 8 : 4;
 }
 
+// Inputs of the decode-step fusion (RoPE of the new token, its append to the
+// pools and attention over the cache including it) run by the single-split
+// kernel.
+struct StepArgs {
+  const void* k;  // new key of (b, kv head h): k + b*k_sb + h*k_sh, head_dim contiguous
+  const void* v;
+  int64_t k_sb, k_sh, v_sb, v_sh;
+  const void* cos;  // RoPE tables: row p at cos + p*cs, full head_dim width
+  const void* sin;
+  int64_t cs, ss;
+  int table_rows;
+  void* kp;  // the pools, written at the new token's slot
+  void* vp;
+  int32_t* seq_lens;  // advanced by one per sequence
+  int32_t* counters;  // [B]: zero on entry, zero again on return
+};
+
 // Single-split decode (max_splits == 1) for page_size % 32 == 0: one
 // workgroup of W waves per (b, kv head, group of <= 16 query heads). The
 // sequence's 32-token steps are dealt out evenly to the W waves by its
@@ -430,17 +451,35 @@ constexpr int cluster_waves() {
 //   M = max_w m_w, out = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w,
 //   lse = (M + log2 sum_w 2^(m_w - M) l_w) * ln 2.
 // The host takes this path only when every wave's range touches <= 64 pages.
-template <typename T, int DPAD, bool HB>
+//
+// STEP (decode-step fusion; D % 16 == 0): q, k and v are the new token's
+// unrotated projections and p = seq_lens[b] its position. q and k are rotated
+// at p (tables at row min(p, table_rows - 1)) and rounded to T; the cache
+// tokens [0, min(max(p, 0), capacity)) are attended as above, and the new
+// token joins the merge as one more partial (m = its score, l = 1, o = v)
+// when 0 <= p < capacity and its page entry is valid, in which case the
+// head-group-0 workgroup also writes the rotated k and v at slot p. The last
+// workgroup of sequence b to finish (a ticket on counters[b]) sets
+// seq_lens[b] = p + 1 and returns counters[b] to zero; every workgroup takes
+// its ticket after its last read of seq_lens[b]. Results equal the RoPE,
+// append and decode launches in sequence, up to fp32 summation order.
+template <typename T, int DPAD, bool HB, bool STEP>
 __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_cluster_kernel(
-    DecodeArgs a, T* __restrict__ out, int64_t o_sb, int64_t o_sh, float* __restrict__ lse_out) {
+    DecodeArgs a, T* __restrict__ out, int64_t o_sb, int64_t o_sh, float* __restrict__ lse_out,
+    StepArgs sa) {
   typedef typename MfmaOps<T>::v8 v8;
   constexpr int W = cluster_waves<DPAD>();
+  constexpr int KS = DPAD / 32;
   constexpr int DT = DPAD / 16;
   constexpr int LROW = DPAD + 16;
   constexpr int TILE = kStep * LROW;  // elements of one K or V tile
   constexpr int OP = DPAD + 4;        // fp32 pitch of a head's row in the merge buffer
+  constexpr int PER_HEAD = DPAD / 4;  // merge items (4 elements each) per head
+  constexpr int IPT = (16 * PER_HEAD + 64 * W - 1) / (64 * W);  // merge items per thread
   static_assert(16 * OP * 4 + 32 * 4 <= 2 * TILE * (int)sizeof(T),
                 "a wave's merge record must fit in its K/V tiles");
+  static_assert(PER_HEAD <= 64 && (PER_HEAD & (PER_HEAD - 1)) == 0,
+                "a head's merge items are one power-of-two group of lanes");
   __shared__ __align__(16) T lds[W * 2 * TILE];
 
   const int wave = threadIdx.x >> 6;
@@ -448,7 +487,11 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   const int kvh = blockIdx.x / a.n_hgroups;
   const int hg = blockIdx.x - kvh * a.n_hgroups;
   const int b = blockIdx.y;
-  const int len = seq_len_of(a, b);
+  const int cap = a.max_pages * a.P;
+  const int p_new = STEP ? a.seq_lens[b] : 0;  // the new token's position
+  const int len = STEP ? min(max(p_new, 0), cap) : seq_len_of(a, b);
+  const int prow = p_new < 0 ? 0 : min(p_new, sa.table_rows - 1);
+  const int half = a.D / 2;
   const int nsteps = (len + kStep - 1) / kStep;
   const int t_begin = (wave * nsteps / W) * kStep;
   const int t_end = min(len, ((wave + 1) * nsteps / W) * kStep);
@@ -459,6 +502,45 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   const bool head_ok = g < a.G;
   const int h = kvh * a.G + g;
 
+  // STEP: the new token's slot, and this thread's merge items' operands
+  // (4 elements each of q, k, their RoPE partners, cos, sin and v), loaded
+  // before the main pass.
+  bool nt_ok = false;
+  int64_t nt_off = 0;
+  u32x2_t nq[IPT], nqp[IPT], nk[IPT], nkp[IPT], nc[IPT], ns[IPT], nv[IPT];
+  if constexpr (STEP) {
+    if (p_new >= 0 && p_new < cap) {
+      const int pi = a.p_shift >= 0 ? (p_new >> a.p_shift) : (p_new / a.P);
+      const int phys = a.bt[(int64_t)b * a.bt_stride + pi];
+      nt_ok = static_cast<unsigned>(phys) < static_cast<unsigned>(a.num_pages);
+      nt_off = (int64_t)phys * a.s_page + (int64_t)kvh * a.s_head +
+               (int64_t)(p_new - pi * a.P) * a.s_tok;
+    }
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int item = threadIdx.x + j * 64 * W;
+      const int hc = item / PER_HEAD;
+      const int d0 = (item - hc * PER_HEAD) * 4;
+      const bool dok = hc < 16 && d0 < a.D;
+      const bool qok = dok && hg * 16 + hc < a.G;
+      const int pd = d0 < half ? d0 + half : d0 - half;
+      const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                    (int64_t)(kvh * a.G + hg * 16 + hc) * a.q_sh;
+      const T* kh = static_cast<const T*>(sa.k) + (int64_t)b * sa.k_sb + (int64_t)kvh * sa.k_sh;
+      const T* vh = static_cast<const T*>(sa.v) + (int64_t)b * sa.v_sb + (int64_t)kvh * sa.v_sh;
+      const T* cr = static_cast<const T*>(sa.cos) + (int64_t)prow * sa.cs;
+      const T* sr = static_cast<const T*>(sa.sin) + (int64_t)prow * sa.ss;
+      const u32x2_t z = {0u, 0u};
+      nq[j] = qok ? *reinterpret_cast<const u32x2_t*>(qh + d0) : z;
+      nqp[j] = qok ? *reinterpret_cast<const u32x2_t*>(qh + pd) : z;
+      nk[j] = dok ? *reinterpret_cast<const u32x2_t*>(kh + d0) : z;
+      nkp[j] = dok ? *reinterpret_cast<const u32x2_t*>(kh + pd) : z;
+      nc[j] = dok ? *reinterpret_cast<const u32x2_t*>(cr + d0) : z;
+      ns[j] = dok ? *reinterpret_cast<const u32x2_t*>(sr + d0) : z;
+      nv[j] = dok ? *reinterpret_cast<const u32x2_t*>(vh + d0) : z;
+    }
+  }
+
   f32x4_t o[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -466,11 +548,50 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   float l_lane = 0.f;
   T* my_k = lds + wave * 2 * TILE;
   T* my_v = my_k + TILE;
-  if (t_begin < t_end)
-    rows_range<T, DPAD, HB>(
-        a, b, kvh, h, head_ok, t_begin, t_end,
-        [&](v8 (&qop)[DPAD / 32]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); }, my_k, my_v,
-        o, m_ref, l_lane);
+  if (t_begin < t_end) {
+    if constexpr (STEP) {
+      // Query operands rotated at p: the lane's 8-element chunks, their
+      // partners half a row away, and the table rows.
+      v8 qpart[KS], cq[KS], sq[KS];
+      const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+      const T* cr = static_cast<const T*>(sa.cos) + (int64_t)prow * sa.cs;
+      const T* sr = static_cast<const T*>(sa.sin) + (int64_t)prow * sa.ss;
+      rows_range<T, DPAD, HB>(
+          a, b, kvh, h, head_ok, t_begin, t_end,
+          [&](v8 (&qop)[KS]) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+              const int d0 = s * 32 + q4 * 8;
+              const bool ok = head_ok && d0 < a.D;
+              const int pd = d0 < half ? d0 + half : d0 - half;
+              qop[s] = ok ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
+              qpart[s] = ok ? *reinterpret_cast<const v8*>(qh + pd) : v8{};
+              cq[s] = ok ? *reinterpret_cast<const v8*>(cr + d0) : v8{};
+              sq[s] = ok ? *reinterpret_cast<const v8*>(sr + d0) : v8{};
+            }
+          },
+          [&](v8 (&qop)[KS]) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+              const bool lo = s * 32 + q4 * 8 < half;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float x = static_cast<float>(qop[s][e]);
+                const float xp = static_cast<float>(qpart[s][e]);
+                const float c = static_cast<float>(cq[s][e]);
+                const float sn = static_cast<float>(sq[s][e]);
+                qop[s][e] = static_cast<T>(lo ? lc_rope_lo(x, xp, c, sn) : lc_rope_hi(xp, x, c, sn));
+              }
+            }
+          },
+          my_k, my_v, o, m_ref, l_lane);
+    } else {
+      rows_range<T, DPAD, HB>(
+          a, b, kvh, h, head_ok, t_begin, t_end,
+          [&](v8 (&qop)[KS]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); },
+          [](v8 (&)[KS]) {}, my_k, my_v, o, m_ref, l_lane);
+    }
+  }
 
   // This wave's record, over its own (now idle) tiles: o [16 heads][OP] fp32,
   // then m [16] and l [16].
@@ -484,16 +605,61 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
     rec[16 * OP + col] = m_ref;
     rec[16 * OP + 16 + col] = l_tot;
   }
+
+  // STEP: rotate this thread's new-token items, write the new k and v (head
+  // group 0, head 0's items cover the row), and form the new token's score of
+  // each item's head (a dot product over the head's PER_HEAD lanes).
+  float s_new[IPT], v_new[IPT][4];
+  if constexpr (STEP) {
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int item = threadIdx.x + j * 64 * W;
+      const int hc = item / PER_HEAD;
+      const int d0 = (item - hc * PER_HEAD) * 4;
+      const bool lo = d0 < half;
+      typedef __attribute__((__vector_size__(4 * sizeof(T)))) T t4;
+      const t4 xq = __builtin_bit_cast(t4, nq[j]), xqp = __builtin_bit_cast(t4, nqp[j]);
+      const t4 xk = __builtin_bit_cast(t4, nk[j]), xkp = __builtin_bit_cast(t4, nkp[j]);
+      const t4 xc = __builtin_bit_cast(t4, nc[j]), xs = __builtin_bit_cast(t4, ns[j]);
+      const t4 xv = __builtin_bit_cast(t4, nv[j]);
+      t4 kr;
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float c = static_cast<float>(xc[e]), sn = static_cast<float>(xs[e]);
+        const float q0 = static_cast<float>(xq[e]), q1 = static_cast<float>(xqp[e]);
+        const float k0 = static_cast<float>(xk[e]), k1 = static_cast<float>(xkp[e]);
+        const T qr = static_cast<T>(lo ? lc_rope_lo(q0, q1, c, sn) : lc_rope_hi(q1, q0, c, sn));
+        kr[e] = static_cast<T>(lo ? lc_rope_lo(k0, k1, c, sn) : lc_rope_hi(k1, k0, c, sn));
+        dot = fmaf(static_cast<float>(qr), static_cast<float>(kr[e]), dot);
+        v_new[j][e] = static_cast<float>(xv[e]);
+      }
+#pragma unroll
+      for (int off = 1; off < PER_HEAD; off <<= 1) dot += __shfl_xor(dot, off, 64);
+      const int gg = hg * 16 + hc;
+      float sc = dot * a.scale_log2;
+      if constexpr (HB) {
+        if (nt_ok && hc < 16 && gg < a.G) sc += decode_bias(a, b, kvh * a.G + gg, p_new);
+      }
+      s_new[j] = nt_ok ? sc : -INFINITY;
+      if (nt_ok && hg == 0 && hc == 0 && d0 < a.D) {
+        *reinterpret_cast<u32x2_t*>(static_cast<T*>(sa.kp) + nt_off + d0) =
+            __builtin_bit_cast(u32x2_t, kr);
+        *reinterpret_cast<u32x2_t*>(static_cast<T*>(sa.vp) + nt_off + d0) = nv[j];
+      }
+    }
+  }
   __syncthreads();
 
   // Combine: each thread owns 4 consecutive elements of one head's row.
-  constexpr int PER_HEAD = DPAD / 4;
-  for (int item = threadIdx.x; item < 16 * PER_HEAD; item += 64 * W) {
+#pragma unroll
+  for (int j = 0; j < IPT; ++j) {
+    const int item = threadIdx.x + j * 64 * W;
     const int hc = item / PER_HEAD;
     const int d0 = (item - hc * PER_HEAD) * 4;
     const int gg = hg * 16 + hc;
-    if (gg >= a.G || d0 >= a.D) continue;
-    float mw[W], mx = -INFINITY;
+    if (hc >= 16 || gg >= a.G || d0 >= a.D) continue;
+    float mw[W], mx = STEP ? s_new[j] : -INFINITY;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       mw[w] = reinterpret_cast<const float*>(lds + w * 2 * TILE)[16 * OP + hc];
@@ -510,6 +676,12 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(e, ow[i], acc[i]);
       }
+      if constexpr (STEP) {
+        const float e = s_new[j] == -INFINITY ? 0.f : lc_exp2(s_new[j] - mx);
+        lsum += e;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(e, v_new[j][i], acc[i]);
+      }
     }
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     const int hh = kvh * a.G + gg;
@@ -519,6 +691,20 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
       if (d0 + i < a.D) oh[i] = lc_from_f32<T>(acc[i] * inv);
     if (lse_out != nullptr && d0 == 0)
       lse_out[(int64_t)b * a.Hq + hh] = lsum > 0.f ? (mx + lc_log2(lsum)) * kLn2 : -INFINITY;
+  }
+
+  if constexpr (STEP) {
+    // Every wave of this workgroup read seq_lens[b] before the barrier above.
+    if (threadIdx.x == 0) {
+      const int n_wg = a.Hkv * a.n_hgroups;
+      const int ticket = __hip_atomic_fetch_add(sa.counters + b, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      if (ticket == n_wg - 1) {
+        __hip_atomic_store(sa.counters + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sa.seq_lens + b, p_new + 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 }
 
@@ -780,11 +966,37 @@ int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, f
   dim3 grid(a.Hkv * a.n_hgroups, a.B);
   const unsigned threads = 64 * cluster_waves<DPAD>();
   T* o = static_cast<T*>(out);
+  const StepArgs none{};
   if (a.bias != nullptr)
-    paged_decode_cluster_kernel<T, DPAD, true><<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse);
+    paged_decode_cluster_kernel<T, DPAD, true, false>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
   else
-    paged_decode_cluster_kernel<T, DPAD, false><<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse);
+    paged_decode_cluster_kernel<T, DPAD, false, false>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
   return lc_check_launch("lc_paged_decode_fwd (single split)");
+}
+
+template <typename T, int DPAD>
+int launch_step(const DecodeArgs& a, const StepArgs& sa, void* out, int64_t o_sb, int64_t o_sh,
+                float* lse, hipStream_t st) {
+  dim3 grid(a.Hkv * a.n_hgroups, a.B);
+  const unsigned threads = 64 * cluster_waves<DPAD>();
+  T* o = static_cast<T*>(out);
+  if (a.bias != nullptr)
+    paged_decode_cluster_kernel<T, DPAD, true, true>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, sa);
+  else
+    paged_decode_cluster_kernel<T, DPAD, false, true>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, sa);
+  return lc_check_launch("lc_paged_decode_step");
+}
+
+template <typename T>
+int launch_step_d(const DecodeArgs& a, const StepArgs& sa, void* out, int64_t o_sb,
+                  int64_t o_sh, float* lse, hipStream_t st) {
+  if (a.D <= 64) return launch_step<T, 64>(a, sa, out, o_sb, o_sh, lse, st);
+  if (a.D <= 128) return launch_step<T, 128>(a, sa, out, o_sb, o_sh, lse, st);
+  return launch_step<T, 256>(a, sa, out, o_sb, o_sh, lse, st);
 }
 
 template <typename T>
@@ -928,6 +1140,124 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
   }
 }
 
+// Validates and launches the decode-step fusion (the single-split kernel's
+// STEP mode).
+int paged_decode_step_impl(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
+                           int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh,
+                           const void* cos, const void* sin, int64_t cos_stride,
+                           int64_t sin_stride, int64_t table_rows, void* key_pages,
+                           void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
+                           int64_t kv_s_tok, const int32_t* block_table, int64_t bt_stride,
+                           int64_t max_pages_per_seq, int64_t num_pages, int32_t* seq_lens,
+                           int32_t* counters, void* out, int64_t o_sb, int64_t o_sh, float* lse,
+                           const void* bias, int64_t bias_sb, int64_t bias_sh, int64_t bias_len,
+                           int bias_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                           int64_t page_size, float scale, int dtype, void* stream) {
+  static const char* who = "lc_paged_decode_step";
+  LC_REQUIRE(B >= 0 && B < 65536, "%s: batch %lld out of range", who, (long long)B);
+  if (B == 0) return LC_OK;
+  LC_REQUIRE(q && k && v && cos && sin && key_pages && value_pages && block_table && seq_lens &&
+                 counters && out,
+             "%s: null pointer", who);
+  LC_REQUIRE(dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16,
+             "%s: dtype must be bf16 or f16 (got %d)", who, dtype);
+  LC_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
+             "%s: n_heads (%lld) must be a multiple of n_kv_heads (%lld)", who, (long long)Hq,
+             (long long)Hkv);
+  LC_REQUIRE(D >= 16 && D <= 256 && D % 16 == 0,
+             "%s: head_dim %lld must be a multiple of 16 in [16, 256]", who, (long long)D);
+  LC_REQUIRE(page_size > 0 && page_size % 32 == 0 && max_pages_per_seq > 0 && num_pages > 0,
+             "%s: page_size must be a positive multiple of 32, max_pages_per_seq and num_pages "
+             "> 0", who);
+  const int64_t cap = max_pages_per_seq * page_size;
+  LC_REQUIRE(cap < (1LL << 31) && num_pages < (1LL << 31),
+             "%s: cache too large for 32-bit token indices", who);
+  LC_REQUIRE(bt_stride >= max_pages_per_seq, "%s: bt_stride < row length", who);
+  const int64_t waves = D <= 128 ? cluster_waves<128>() : cluster_waves<256>();
+  const int64_t wave_tokens = ((cap + kStep - 1) / kStep + waves - 1) / waves * kStep;
+  LC_REQUIRE((wave_tokens - 1) / page_size + 2 <= 64,
+             "%s: a capacity of %lld tokens is too large for the one-workgroup-per-sequence "
+             "kernel (each of its %lld waves covers at most 64 pages); use lc_rope_kv_append "
+             "and lc_paged_decode_fwd",
+             who, (long long)cap, (long long)waves);
+  LC_REQUIRE(((page_size - 1) * kv_s_tok + D) * 2 < (1LL << 31),
+             "%s: a page's head slice exceeds 2 GiB", who);
+  LC_REQUIRE(table_rows >= cap && table_rows < (1LL << 31),
+             "%s: the cos/sin tables (%lld rows) must cover the block-table capacity (%lld "
+             "positions)",
+             who, (long long)table_rows, (long long)cap);
+  LC_REQUIRE(q_sb >= 0 && q_sh >= 0 && k_sb >= 0 && k_sh >= 0 && v_sb >= 0 && v_sh >= 0 &&
+                 cos_stride >= 0 && sin_stride >= 0 && kv_s_page >= 0 && kv_s_head >= 0 &&
+                 kv_s_tok >= 0,
+             "%s: negative stride", who);
+  LC_REQUIRE(lc_aligned(q, 16) && q_sb % 8 == 0 && q_sh % 8 == 0 && lc_aligned(cos, 16) &&
+                 lc_aligned(sin, 16) && cos_stride % 8 == 0 && sin_stride % 8 == 0 &&
+                 lc_aligned(key_pages, 16) && lc_aligned(value_pages, 16) &&
+                 kv_s_page % 8 == 0 && kv_s_head % 8 == 0 && kv_s_tok % 8 == 0,
+             "%s: q, the cos/sin tables and the pools need 16-byte alignment and strides in "
+             "multiples of 8 elements", who);
+  LC_REQUIRE(lc_aligned(k, 8) && lc_aligned(v, 8) && k_sb % 4 == 0 && k_sh % 4 == 0 &&
+                 v_sb % 4 == 0 && v_sh % 4 == 0,
+             "%s: k and v need 8-byte alignment and strides in multiples of 4 elements", who);
+  LC_REQUIRE(bias == nullptr || (bias_sb >= 0 && bias_sh >= 0 && bias_len >= 0 &&
+                                 bias_len < (1LL << 31)),
+             "%s: bad bias strides or length", who);
+  LC_REQUIRE(bias == nullptr || bias_dtype == LC_DTYPE_F32 || bias_dtype == LC_DTYPE_F16 ||
+                 bias_dtype == LC_DTYPE_BF16,
+             "%s: unknown bias dtype %d", who, bias_dtype);
+
+  DecodeArgs a{};
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.kp = key_pages;
+  a.vp = value_pages;
+  a.s_page = kv_s_page;
+  a.s_head = kv_s_head;
+  a.s_tok = kv_s_tok;
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.max_pages = static_cast<int>(max_pages_per_seq);
+  a.num_pages = static_cast<int>(num_pages);
+  a.seq_lens = seq_lens;
+  a.B = static_cast<int>(B);
+  a.Hq = static_cast<int>(Hq);
+  a.Hkv = static_cast<int>(Hkv);
+  a.G = static_cast<int>(Hq / Hkv);
+  a.D = static_cast<int>(D);
+  a.P = static_cast<int>(page_size);
+  a.p_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctzll(page_size) : -1;
+  a.split_tokens = static_cast<int>((cap + 63) / 64 * 64);
+  a.max_splits = 1;
+  a.n_hgroups = (a.G + 15) / 16;
+  a.scale_log2 = scale * kLog2e;
+  a.bias = bias_len > 0 ? bias : nullptr;
+  a.bias_sb = bias_sb;
+  a.bias_sh = bias_sh;
+  a.bias_len = static_cast<int>(bias_len);
+  a.bias_dtype = bias_dtype;
+
+  StepArgs sa{};
+  sa.k = k;
+  sa.v = v;
+  sa.k_sb = k_sb;
+  sa.k_sh = k_sh;
+  sa.v_sb = v_sb;
+  sa.v_sh = v_sh;
+  sa.cos = cos;
+  sa.sin = sin;
+  sa.cs = cos_stride;
+  sa.ss = sin_stride;
+  sa.table_rows = static_cast<int>(table_rows);
+  sa.kp = key_pages;
+  sa.vp = value_pages;
+  sa.seq_lens = seq_lens;
+  sa.counters = counters;
+  hipStream_t st = lc_stream(stream);
+  if (dtype == LC_DTYPE_BF16) return launch_step_d<bf16_t>(a, sa, out, o_sb, o_sh, lse, st);
+  return launch_step_d<f16_t>(a, sa, out, o_sb, o_sh, lse, st);
+}
+
 // Device scratch of lc_paged_decode_fwd_noalloc, one per device (its address
 // differs per device). Host code uses the address kept in g_scratch_ptr, never
 // the symbol itself (on the host the name is only a handle).
@@ -1035,6 +1365,25 @@ int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
                            seq_lens, out, o_sb, o_sh, lse, bias, bias_sb, bias_sh, bias_len,
                            bias_dtype, ws, LC_DECODE_NOALLOC_SCRATCH_BYTES, B, Hq, Hkv, D,
                            page_size, split_tokens, max_splits, scale, dtype, stream);
+}
+
+int lc_paged_decode_step(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
+                         int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh,
+                         const void* cos, const void* sin, int64_t cos_stride, int64_t sin_stride,
+                         int64_t table_rows, void* key_pages, void* value_pages,
+                         int64_t kv_s_page, int64_t kv_s_head, int64_t kv_s_tok,
+                         const int32_t* block_table, int64_t bt_stride,
+                         int64_t max_pages_per_seq, int64_t num_pages, int32_t* seq_lens,
+                         int32_t* counters, void* out, int64_t o_sb, int64_t o_sh, float* lse,
+                         const void* bias, int64_t bias_sb, int64_t bias_sh, int64_t bias_len,
+                         int bias_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                         int64_t page_size, float scale, int dtype, void* stream) {
+  return paged_decode_step_impl(q, q_sb, q_sh, k, k_sb, k_sh, v, v_sb, v_sh, cos, sin,
+                                cos_stride, sin_stride, table_rows, key_pages, value_pages,
+                                kv_s_page, kv_s_head, kv_s_tok, block_table, bt_stride,
+                                max_pages_per_seq, num_pages, seq_lens, counters, out, o_sb, o_sh,
+                                lse, bias, bias_sb, bias_sh, bias_len, bias_dtype, B, Hq, Hkv, D,
+                                page_size, scale, dtype, stream);
 }
 
 }  // extern "C"

@@ -252,8 +252,8 @@ __global__ __launch_bounds__(1024) void rope_kv_append_kernel(KvPool pool, RopeA
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float x1 = lc_to_f32(xa.v[e]), x2 = lc_to_f32(xb.v[e]);
-      o1.v[e] = lc_from_f32<T>(x1 * lc_to_f32(ca.v[e]) - x2 * lc_to_f32(sa.v[e]));
-      o2.v[e] = lc_from_f32<T>(x2 * lc_to_f32(cb.v[e]) + x1 * lc_to_f32(sb.v[e]));
+      o1.v[e] = lc_from_f32<T>(lc_rope_lo(x1, x2, lc_to_f32(ca.v[e]), lc_to_f32(sa.v[e])));
+      o2.v[e] = lc_from_f32<T>(lc_rope_hi(x1, x2, lc_to_f32(cb.v[e]), lc_to_f32(sb.v[e])));
     }
     T* dst = kind == 1 ? static_cast<T*>(pool.kp) + off
                        : static_cast<T*>(a.qo) + b * a.qos[0] + h * a.qos[1] + s * a.qos[2];

@@ -97,6 +97,13 @@ _SIGNATURES = {
          _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_p],
     ),
+    "lc_paged_decode_step": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64,
+         _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p,
+         _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, ctypes.c_int, _c_p],
+    ),
     "lc_paged_kv_gather": (
         ctypes.c_int,
         [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64,

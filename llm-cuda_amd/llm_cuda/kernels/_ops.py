@@ -704,6 +704,96 @@ def _rope_kv_append(q, k, v, cos, sin, key_pages, value_pages, block_table, seq_
     return q_out
 
 
+def decode_step_supported(dtype: torch.dtype, head_dim: int, page_size: int,
+                          capacity_tokens: int) -> bool:
+    """Whether lc_paged_decode_step takes these sizes (bf16/f16, head_dim a
+    multiple of 16 up to 256, and the single-split kernel's page rule)."""
+    return (dtype in (torch.bfloat16, torch.float16) and head_dim % 16 == 0
+            and 16 <= head_dim <= 256
+            and single_split_fits(capacity_tokens, page_size, head_dim))
+
+
+def paged_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                      sin: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
+                      block_table: torch.Tensor, seq_lens: torch.Tensor, counters: torch.Tensor,
+                      scale: float | None = None, attention_mask: torch.Tensor | None = None,
+                      return_lse: bool = False):
+    """RoPE of the new token at p = seq_lens[b], its append to the page pools and
+    decode attention over the cache including it, in one launch; seq_lens
+    advances by one in place.
+
+    q [B, Hq, 1, D], k and v [B, Hkv, 1, D] (unrotated projections); cos/sin
+    full tables indexed by position covering the block-table capacity;
+    counters: int32 [B] zeros (left at zero). attention_mask as in
+    paged_decode over token indices 0 .. p. Returns out [B, Hq, 1, D] (a view
+    of a [B, 1, Hq, D] buffer) and lse [B, Hq] if return_lse. Forward only.
+    """
+    args = (cos, sin, key_pages, value_pages, block_table, seq_lens, counters, scale,
+            attention_mask, return_lse)
+    if _records_grad(q, k, v):
+        return _ForwardOnly.apply("paged_decode_step",
+                                  lambda a, b, c: _paged_decode_step(a, b, c, *args), q, k, v)
+    return _paged_decode_step(q, k, v, *args)
+
+
+def _paged_decode_step(q, k, v, cos, sin, key_pages, value_pages, block_table, seq_lens,
+                       counters, scale, attention_mask, return_lse):
+    _pool_checks(key_pages, value_pages, block_table)
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape or q.shape[2] != 1:
+        raise ValueError("q must be [B, Hq, 1, D] and k, v [B, Hkv, 1, D]")
+    B, Hq, _, D = q.shape
+    N, Hkv, P, Dp = key_pages.shape
+    if k.shape != (B, Hkv, 1, D) or Dp != D or block_table.shape[0] != B:
+        raise ValueError("q/k/v do not match the cache layout")
+    if Hq % Hkv != 0:
+        raise ValueError(f"n_heads ({Hq}) must be a multiple of n_kv_heads ({Hkv})")
+    for name, t in (("seq_lens", seq_lens), ("counters", counters)):
+        if t.dtype != torch.int32 or t.shape != (B,) or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous int32 [batch] tensor")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D:
+        raise ValueError("cos/sin must be [positions, head_dim]")
+    if not (q.dtype == k.dtype == v.dtype == cos.dtype == sin.dtype == key_pages.dtype):
+        raise TypeError("q, k, v, cos, sin and the pools must share a dtype")
+    capacity = block_table.shape[1] * P
+    if not decode_step_supported(q.dtype, D, P, capacity):
+        raise ValueError(
+            f"the fused decode step takes bf16/f16, head_dim a multiple of 16 <= 256 and "
+            f"page_size a multiple of 32 with a capacity the one-workgroup kernel covers; got "
+            f"{q.dtype}, head_dim {D}, page_size {P}, capacity {capacity}")
+    dev = nat.require_device(q, k, v, cos, sin, key_pages, value_pages, block_table, seq_lens,
+                             counters)
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    cos = cos if cos.stride(-1) == 1 else cos.contiguous()
+    sin = sin if sin.stride(-1) == 1 else sin.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    bias = None
+    if attention_mask is not None:
+        nat.require_device(q, attention_mask)
+        bias = decode_bias(attention_mask, B, Hq, q.dtype)
+    buf = torch.empty((B, 1, Hq, D), dtype=q.dtype, device=dev)
+    out = buf.transpose(1, 2)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_paged_decode_step(
+            q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+            v.data_ptr(), v.stride(0), v.stride(1), cos.data_ptr(), sin.data_ptr(),
+            cos.stride(0), sin.stride(0), cos.shape[0], key_pages.data_ptr(),
+            value_pages.data_ptr(), key_pages.stride(0), key_pages.stride(1), key_pages.stride(2),
+            block_table.data_ptr(), block_table.stride(0), block_table.shape[1], N,
+            seq_lens.data_ptr(), counters.data_ptr(), out.data_ptr(), out.stride(0),
+            out.stride(1), None if lse is None else lse.data_ptr(),
+            None if bias is None else bias.data_ptr(), 0 if bias is None else bias.stride(0),
+            0 if bias is None else bias.stride(1), 0 if bias is None else bias.shape[-1],
+            0 if bias is None else nat.lc_dtype(bias), B, Hq, Hkv, D, P, float(scale),
+            nat.lc_dtype(q), _stream(dev))
+    nat.check(rc, "lc_paged_decode_step")
+    return (out, lse) if return_lse else out
+
+
 def kv_gather(key_pages: torch.Tensor, value_pages: torch.Tensor, block_table: torch.Tensor,
               length: int):
     """Contiguous [B, Hkv, length, D] copies of the first `length` tokens."""

@@ -10,9 +10,12 @@ differs only in how the attention itself is computed, all on HIP kernels:
     positions and sliced per call (every row depends only on its position,
     so the slices equal the per-call tables of rotary.py:29-71).
   * Paged cache, one query token (decode): new K/V are scattered into the page
-    pools and the query attends to the pools in place through the block table
-    (split-K flash-decode). The reference instead copied the whole cache into a
-    contiguous tensor every step (kv_cache.py:65-83) and decoded that.
+    pools and the query attends to the pools in place through the block table.
+    For a batch of equal lengths that fills the CUs, RoPE, the append and the
+    attention are one launch (one workgroup per sequence and head group);
+    otherwise RoPE + append is one launch and split-K flash-decode another.
+    The reference instead copied the whole cache into a contiguous tensor
+    every step (kv_cache.py:65-83) and decoded that.
   * Prompt / multi-token chunk: causal prefill attention with native GQA (no
     repeated K/V) and the causal diagonal shifted by the cached prefix length,
     which covers both the reference's fused path (past_len == 0) and its
@@ -130,18 +133,23 @@ class Llama3Attention(nn.Module):
             past_len = 0
 
         if paged and use_cache and seq_len == 1:
-            # Decode step: RoPE and the cache append in one launch, positions
-            # taken from the cache's device-side lengths.
+            # Decode step, positions taken from the cache's device-side lengths:
+            # RoPE, the cache append and the attention in one launch where the
+            # one-workgroup-per-sequence kernel suits the batch, else RoPE and
+            # the append in one launch and split-K decode in another.
             cache = past_key_value
             if attention_mask is not None:
                 self._check_mask(attention_mask, bsz, 1, past_len + 1)
             rows = cache.max_pages * cache.page_size
             self._rope_tables(0, rows, x.device, x.dtype)
             cos_t, sin_t = self._rope_cache[2], self._rope_cache[3]
-            q = cache.append_rotated(q, k, v, cos_t, sin_t)
-            out = paged_decode_attention(
-                q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens,
-                attention_mask=attention_mask, uniform_lengths=cache.uniform_lengths)
+            if cache.can_fuse_decode_step(self.num_heads, q.dtype):
+                out = cache.decode_step(q, k, v, cos_t, sin_t, attention_mask=attention_mask)
+            else:
+                q = cache.append_rotated(q, k, v, cos_t, sin_t)
+                out = paged_decode_attention(
+                    q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens,
+                    attention_mask=attention_mask, uniform_lengths=cache.uniform_lengths)
             out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
             return self.o_proj(out), cache
 

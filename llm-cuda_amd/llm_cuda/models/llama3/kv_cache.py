@@ -81,6 +81,8 @@ class PagedKVLayerCache:
             seq_lens.zero_()
         self.seq_lens = seq_lens
         self.lengths = [0] * batch_size
+        # Zeroed scratch of the fused decode step (it leaves the counters at zero).
+        self.step_counters = torch.zeros(batch_size, dtype=torch.int32, device=device)
 
     @property
     def length(self) -> int:
@@ -134,6 +136,46 @@ class PagedKVLayerCache:
                                     self.block_table, self.seq_lens)
         self.lengths = [n + seq for n in self.lengths]
         return q_rot
+
+    def can_fuse_decode_step(self, n_heads: int, dtype: torch.dtype) -> bool:
+        """Whether `decode_step` takes this cache: equal lengths, a head layout
+        whose (sequence, kv head, head group) units fill whole rounds of the
+        CUs, and sizes the fused kernel supports (its single split must be
+        the split the decode heuristic would choose)."""
+        capacity = self.max_pages * self.page_size
+        if not (self.uniform_lengths and self.key_pages.is_cuda
+                and _ops.decode_step_supported(dtype, self.head_dim, self.page_size, capacity)):
+            return False
+        group = n_heads // self.num_kv_heads
+        split = _ops.choose_split_tokens(
+            self.batch_size, self.num_kv_heads, group, capacity, self.page_size, self.head_dim,
+            True, _ops._cu_count(self.key_pages.device))
+        return split >= capacity
+
+    def decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                    return_lse: bool = False):
+        """One decode step of attention in one launch: RoPE of q and k at the
+        positions seq_lens[b], the append of the rotated k and v, and attention
+        of the rotated q over the cache including the new token. Advances the
+        lengths by one and returns out [B, Hq, 1, D] (and the fp32 lse [B, Hq]
+        if return_lse). cos/sin are full tables indexed by position covering
+        max_pages * page_size positions."""
+        if k.shape != v.shape or k.dim() != 4 or q.dim() != 4 or k.shape[2] != 1:
+            raise ValueError("Expected q [batch, heads, 1, head_dim] and k, v [batch, kv_heads, "
+                             "1, head_dim]")
+        if k.shape[0] != self.batch_size or q.shape[0] != self.batch_size:
+            raise ValueError(
+                f"batch {k.shape[0]} does not match the cache batch size {self.batch_size}")
+        if k.shape[1] != self.num_kv_heads or k.shape[3] != self.head_dim:
+            raise ValueError("k/v shapes do not match cache layout")
+        if max(self.lengths) + 1 > self.max_seq_len:
+            raise ValueError("Appending would exceed max_seq_len")
+        res = _ops.paged_decode_step(q, k, v, cos, sin, self.key_pages, self.value_pages,
+                                     self.block_table, self.seq_lens, self.step_counters,
+                                     attention_mask=attention_mask, return_lse=return_lse)
+        self.lengths = [n + 1 for n in self.lengths]
+        return res
 
     def get_kv(self) -> tuple[torch.Tensor, torch.Tensor]:
         length = self.length
