@@ -75,15 +75,60 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
   // the scaling after the reduction waits on no second memory round trip.
   W wcache[ITEMS > 0 ? ITEMS : 1][VEC];
   if constexpr (ITEMS > 0) {
+    // Every load of every item is issued before the first store of s_out
+    // (which x may alias), with no branch between them (items past the row
+    // re-read its last vector), so the items cost one memory round trip.
+    T xraw[ITEMS][VEC], rraw[ITEMS][VEC];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int vi = min(tid + it * nthreads, nvec - 1);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) wcache[it][e] = w[(int64_t)vi * VEC + e];
+      if constexpr (VEC * sizeof(T) == 16) {
+        const Vec16<T> a = EW_LD(xr + (int64_t)vi * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xraw[it][e] = a.v[e];
+        if constexpr (ADD) {
+          const Vec16<T> b = EW_LD(rr + (int64_t)vi * VEC);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) rraw[it][e] = b.v[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          xraw[it][e] = xr[(int64_t)vi * VEC + e];
+          if constexpr (ADD) rraw[it][e] = rr[(int64_t)vi * VEC + e];
+        }
+      }
+    }
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int vi = tid + it * nthreads;
-      if (vi < nvec) {
+      const bool live = vi < nvec;
+      Vec16<T> sum;
+      float sq = 0.f;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) wcache[it][e] = w[(int64_t)vi * VEC + e];
-        load_row(vi, cache[it]);
+      for (int e = 0; e < VEC; ++e) {
+        float v = lc_to_f32(xraw[it][e]);
+        if constexpr (ADD) {
+          const T sv = lc_from_f32<T>(v + lc_to_f32(rraw[it][e]));
+          sum.v[e % Vec16<T>::N] = sv;
+          v = lc_to_f32(sv);
+        }
+        cache[it][e] = v;
+        sq = fmaf(v, v, sq);
+      }
+      acc += live ? sq : 0.f;
+      if constexpr (ADD) {
+        if (live) {
+          if constexpr (VEC * sizeof(T) == 16) {
+            EW_ST(sr + (int64_t)vi * VEC, sum);
+          } else {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc = fmaf(cache[it][e], cache[it][e], acc);
+            for (int e = 0; e < VEC; ++e)
+              sr[(int64_t)vi * VEC + e] = lc_from_f32<T>(cache[it][e]);
+          }
+        }
       }
     }
   } else {
@@ -101,8 +146,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
   if ((tid & 63) == 0) red[wave] = acc;
   __syncthreads();
   float total = 0.f;
-  const int nwaves = nthreads >> 6;
-  for (int i = 0; i < nwaves; ++i) total += red[i];
+  const int nwaves = nthreads >> 6;  // <= 4 (launch bound 256)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) total += i < nwaves ? red[i] : 0.f;
   const float inv_rms = rsqrtf(total / static_cast<float>(hidden) + eps);
 
   if constexpr (ITEMS > 0) {

@@ -236,15 +236,21 @@ __device__ __forceinline__ void store_partial(const DecodeArgs& a, int b, int h,
 }
 
 // Query operands of head h (all zero for a padding head or past head_dim).
+// The loads are unconditional (a padding head or chunk reads head h_safe's
+// chunk 0 instead) and zeroed afterwards, so no branch separates them.
 template <typename T, int DPAD>
-__device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int h, bool head_ok, int q4,
+__device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int h, int h_safe,
+                                       bool head_ok, int q4,
                                        typename MfmaOps<T>::v8 (&qop)[DPAD / 32]) {
   typedef typename MfmaOps<T>::v8 v8;
-  const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+  const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                (int64_t)(head_ok ? h : h_safe) * a.q_sh;
 #pragma unroll
   for (int s = 0; s < DPAD / 32; ++s) {
     const int d0 = s * 32 + q4 * 8;
-    qop[s] = (head_ok && d0 < a.D) ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
+    const bool ok = head_ok && d0 < a.D;
+    const v8 x = *reinterpret_cast<const v8*>(qh + (ok ? d0 : 0));
+    qop[s] = ok ? x : v8{};
   }
 }
 
@@ -257,12 +263,15 @@ __device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int h, bool h
 // first step's K/V loads are issued (a place for arithmetic on the loaded
 // operands that should not hold up that issue). HB: the call carries an
 // additive bias (loaded with the step's K/V, one step ahead).
-template <typename T, int DPAD, bool HB, typename QLoad, typename QFinish>
+// PRE: the caller has loaded the sequence's whole block-table row (max_pages
+// <= 64; entry `lane` per lane, -1 past the row) and passes it as row_entry,
+// so no table load is issued here.
+template <typename T, int DPAD, bool HB, bool PRE = false, typename QLoad, typename QFinish>
 __device__ __forceinline__ void rows_range(const DecodeArgs& a, int b, int kvh, int h,
                                            bool head_ok, int t_begin, int t_end, QLoad load_q,
                                            QFinish finish_q, T* lds_k, T* lds_v,
                                            f32x4_t (&o)[DPAD / 16], float& m_ref,
-                                           float& l_lane) {
+                                           float& l_lane, int row_entry = -2) {
   typedef MfmaOps<T> Ops;
   typedef typename Ops::v8 v8;
   constexpr int KS = DPAD / 32;      // MFMA k-steps over head_dim
@@ -279,11 +288,13 @@ __device__ __forceinline__ void rows_range(const DecodeArgs& a, int b, int kvh, 
   const int schunk = lane % CPR;  // staging: 16-byte chunk within the row
   const bool chunk_in_d = schunk * 8 < a.D;
 
-  // Block-table entries of this range, one per lane.
-  const int first_page = a.p_shift >= 0 ? (t_begin >> a.p_shift) : (t_begin / a.P);
+  // Block-table entries of this range, one per lane (or the preloaded row).
+  const int first_page = PRE ? 0 : (a.p_shift >= 0 ? (t_begin >> a.p_shift) : (t_begin / a.P));
   const int last_page = a.p_shift >= 0 ? ((t_end - 1) >> a.p_shift) : ((t_end - 1) / a.P);
-  const int my_page =
-      first_page + lane <= last_page ? a.bt[(int64_t)b * a.bt_stride + first_page + lane] : -1;
+  int my_page = row_entry;
+  if constexpr (!PRE)
+    my_page =
+        first_page + lane <= last_page ? a.bt[(int64_t)b * a.bt_stride + first_page + lane] : -1;
   v8 qop[KS];
   load_q(qop);
 
@@ -413,7 +424,7 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   float l_lane = 0.f;
   rows_range<T, DPAD, HB>(
       a, b, kvh, h, head_ok, t_begin, t_end,
-      [&](v8 (&qop)[DPAD / 32]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); },
+      [&](v8 (&qop)[DPAD / 32]) { load_q<T, DPAD>(a, b, h, kvh * a.G, head_ok, q4, qop); },
       [](v8 (&)[DPAD / 32]) {}, lds_k, lds_v, o, m_ref, l_lane);
   store_partial<DT>(a, b, h, split, head_ok, q4, m_ref, l_lane, o);
 }
@@ -463,7 +474,7 @@ struct StepArgs {
 // seq_lens[b] = p + 1 and returns counters[b] to zero; every workgroup takes
 // its ticket after its last read of seq_lens[b]. Results equal the RoPE,
 // append and decode launches in sequence, up to fp32 summation order.
-template <typename T, int DPAD, bool HB, bool STEP>
+template <typename T, int DPAD, bool HB, bool STEP, bool PRE>
 __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_cluster_kernel(
     DecodeArgs a, T* __restrict__ out, int64_t o_sb, int64_t o_sh, float* __restrict__ lse_out,
     StepArgs sa) {
@@ -488,8 +499,18 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   const int hg = blockIdx.x - kvh * a.n_hgroups;
   const int b = blockIdx.y;
   const int cap = a.max_pages * a.P;
+  // PRE (max_pages <= 64): the block-table row is loaded whole (one entry per
+  // lane) together with the length, so the first K/V loads wait on one round
+  // trip, not on the length and then the table.
+  int row_entry = -1;
+  if constexpr (PRE) row_entry = a.bt[(int64_t)b * a.bt_stride + min(lane, a.max_pages - 1)];
   const int p_new = STEP ? a.seq_lens[b] : 0;  // the new token's position
   const int len = STEP ? min(max(p_new, 0), cap) : seq_len_of(a, b);
+  if constexpr (PRE) {
+    row_entry = lane < a.max_pages ? row_entry : -1;
+    // Keep the row load here, beside the length's, rather than sunk to its use.
+    asm volatile("" : "+v"(row_entry));
+  }
   const int prow = p_new < 0 ? 0 : min(p_new, sa.table_rows - 1);
   const int half = a.D / 2;
   const int nsteps = (len + kStep - 1) / kStep;
@@ -505,17 +526,17 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   // STEP: the new token's slot, and this thread's merge items' operands
   // (4 elements each of q, k, their RoPE partners, cos, sin and v), loaded
   // before the main pass.
-  bool nt_ok = false;
-  int64_t nt_off = 0;
+  // Every load below is unconditional, from a clamped address, and masked
+  // where it is used, so no branch separates the loads from one another.
+  int nt_phys = -1;
   u32x2_t nq[IPT], nqp[IPT], nk[IPT], nkp[IPT], nc[IPT], ns[IPT], nv[IPT];
   if constexpr (STEP) {
-    if (p_new >= 0 && p_new < cap) {
-      const int pi = a.p_shift >= 0 ? (p_new >> a.p_shift) : (p_new / a.P);
-      const int phys = a.bt[(int64_t)b * a.bt_stride + pi];
-      nt_ok = static_cast<unsigned>(phys) < static_cast<unsigned>(a.num_pages);
-      nt_off = (int64_t)phys * a.s_page + (int64_t)kvh * a.s_head +
-               (int64_t)(p_new - pi * a.P) * a.s_tok;
-    }
+    const int pc = p_new >= 0 && p_new < cap ? p_new : 0;
+    const int pi = a.p_shift >= 0 ? (pc >> a.p_shift) : (pc / a.P);
+    if constexpr (PRE)
+      nt_phys = __builtin_amdgcn_readlane(row_entry, pi);
+    else
+      nt_phys = a.bt[(int64_t)b * a.bt_stride + pi];
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
       const int item = threadIdx.x + j * 64 * W;
@@ -523,21 +544,21 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
       const int d0 = (item - hc * PER_HEAD) * 4;
       const bool dok = hc < 16 && d0 < a.D;
       const bool qok = dok && hg * 16 + hc < a.G;
-      const int pd = d0 < half ? d0 + half : d0 - half;
+      const int dc = dok ? d0 : 0;
+      const int pd = dc < half ? dc + half : dc - half;
       const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                    (int64_t)(kvh * a.G + hg * 16 + hc) * a.q_sh;
+                    (int64_t)(kvh * a.G + (qok ? hg * 16 + hc : 0)) * a.q_sh;
       const T* kh = static_cast<const T*>(sa.k) + (int64_t)b * sa.k_sb + (int64_t)kvh * sa.k_sh;
       const T* vh = static_cast<const T*>(sa.v) + (int64_t)b * sa.v_sb + (int64_t)kvh * sa.v_sh;
       const T* cr = static_cast<const T*>(sa.cos) + (int64_t)prow * sa.cs;
       const T* sr = static_cast<const T*>(sa.sin) + (int64_t)prow * sa.ss;
-      const u32x2_t z = {0u, 0u};
-      nq[j] = qok ? *reinterpret_cast<const u32x2_t*>(qh + d0) : z;
-      nqp[j] = qok ? *reinterpret_cast<const u32x2_t*>(qh + pd) : z;
-      nk[j] = dok ? *reinterpret_cast<const u32x2_t*>(kh + d0) : z;
-      nkp[j] = dok ? *reinterpret_cast<const u32x2_t*>(kh + pd) : z;
-      nc[j] = dok ? *reinterpret_cast<const u32x2_t*>(cr + d0) : z;
-      ns[j] = dok ? *reinterpret_cast<const u32x2_t*>(sr + d0) : z;
-      nv[j] = dok ? *reinterpret_cast<const u32x2_t*>(vh + d0) : z;
+      nq[j] = *reinterpret_cast<const u32x2_t*>(qh + dc);
+      nqp[j] = *reinterpret_cast<const u32x2_t*>(qh + pd);
+      nk[j] = *reinterpret_cast<const u32x2_t*>(kh + dc);
+      nkp[j] = *reinterpret_cast<const u32x2_t*>(kh + pd);
+      nc[j] = *reinterpret_cast<const u32x2_t*>(cr + dc);
+      ns[j] = *reinterpret_cast<const u32x2_t*>(sr + dc);
+      nv[j] = *reinterpret_cast<const u32x2_t*>(vh + dc);
     }
   }
 
@@ -553,43 +574,47 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
       // Query operands rotated at p: the lane's 8-element chunks, their
       // partners half a row away, and the table rows.
       v8 qpart[KS], cq[KS], sq[KS];
-      const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+      const T* qh = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                    (int64_t)(head_ok ? h : kvh * a.G) * a.q_sh;
       const T* cr = static_cast<const T*>(sa.cos) + (int64_t)prow * sa.cs;
       const T* sr = static_cast<const T*>(sa.sin) + (int64_t)prow * sa.ss;
-      rows_range<T, DPAD, HB>(
+      rows_range<T, DPAD, HB, PRE>(
           a, b, kvh, h, head_ok, t_begin, t_end,
           [&](v8 (&qop)[KS]) {
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
               const int d0 = s * 32 + q4 * 8;
-              const bool ok = head_ok && d0 < a.D;
-              const int pd = d0 < half ? d0 + half : d0 - half;
-              qop[s] = ok ? *reinterpret_cast<const v8*>(qh + d0) : v8{};
-              qpart[s] = ok ? *reinterpret_cast<const v8*>(qh + pd) : v8{};
-              cq[s] = ok ? *reinterpret_cast<const v8*>(cr + d0) : v8{};
-              sq[s] = ok ? *reinterpret_cast<const v8*>(sr + d0) : v8{};
+              const int dc = head_ok && d0 < a.D ? d0 : 0;
+              const int pd = dc < half ? dc + half : dc - half;
+              qop[s] = *reinterpret_cast<const v8*>(qh + dc);
+              qpart[s] = *reinterpret_cast<const v8*>(qh + pd);
+              cq[s] = *reinterpret_cast<const v8*>(cr + dc);
+              sq[s] = *reinterpret_cast<const v8*>(sr + dc);
             }
           },
           [&](v8 (&qop)[KS]) {
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-              const bool lo = s * 32 + q4 * 8 < half;
+              const int d0 = s * 32 + q4 * 8;
+              const bool ok = head_ok && d0 < a.D;
+              const bool lo = d0 < half;
 #pragma unroll
               for (int e = 0; e < 8; ++e) {
                 const float x = static_cast<float>(qop[s][e]);
                 const float xp = static_cast<float>(qpart[s][e]);
                 const float c = static_cast<float>(cq[s][e]);
                 const float sn = static_cast<float>(sq[s][e]);
-                qop[s][e] = static_cast<T>(lo ? lc_rope_lo(x, xp, c, sn) : lc_rope_hi(xp, x, c, sn));
+                const T r = static_cast<T>(lo ? lc_rope_lo(x, xp, c, sn) : lc_rope_hi(xp, x, c, sn));
+                qop[s][e] = ok ? r : static_cast<T>(0.f);
               }
             }
           },
-          my_k, my_v, o, m_ref, l_lane);
+          my_k, my_v, o, m_ref, l_lane, row_entry);
     } else {
-      rows_range<T, DPAD, HB>(
+      rows_range<T, DPAD, HB, PRE>(
           a, b, kvh, h, head_ok, t_begin, t_end,
-          [&](v8 (&qop)[KS]) { load_q<T, DPAD>(a, b, h, head_ok, q4, qop); },
-          [](v8 (&)[KS]) {}, my_k, my_v, o, m_ref, l_lane);
+          [&](v8 (&qop)[KS]) { load_q<T, DPAD>(a, b, h, kvh * a.G, head_ok, q4, qop); },
+          [](v8 (&)[KS]) {}, my_k, my_v, o, m_ref, l_lane, row_entry);
     }
   }
 
@@ -610,12 +635,23 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   // group 0, head 0's items cover the row), and form the new token's score of
   // each item's head (a dot product over the head's PER_HEAD lanes).
   float s_new[IPT], v_new[IPT][4];
+  bool nt_ok = false;
+  int64_t nt_off = 0;
   if constexpr (STEP) {
+    // The new token is attended and stored iff it is inside the capacity and
+    // its page entry is valid.
+    nt_ok = p_new >= 0 && p_new < cap &&
+            static_cast<unsigned>(nt_phys) < static_cast<unsigned>(a.num_pages);
+    const int pi = a.p_shift >= 0 ? (p_new >> a.p_shift) : (p_new / a.P);
+    nt_off = (int64_t)nt_phys * a.s_page + (int64_t)kvh * a.s_head +
+             (int64_t)(p_new - pi * a.P) * a.s_tok;
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
       const int item = threadIdx.x + j * 64 * W;
       const int hc = item / PER_HEAD;
       const int d0 = (item - hc * PER_HEAD) * 4;
+      const bool dok = hc < 16 && d0 < a.D;
+      const bool qok = dok && hg * 16 + hc < a.G;
       const bool lo = d0 < half;
       typedef __attribute__((__vector_size__(4 * sizeof(T)))) T t4;
       const t4 xq = __builtin_bit_cast(t4, nq[j]), xqp = __builtin_bit_cast(t4, nqp[j]);
@@ -631,7 +667,7 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
         const float k0 = static_cast<float>(xk[e]), k1 = static_cast<float>(xkp[e]);
         const T qr = static_cast<T>(lo ? lc_rope_lo(q0, q1, c, sn) : lc_rope_hi(q1, q0, c, sn));
         kr[e] = static_cast<T>(lo ? lc_rope_lo(k0, k1, c, sn) : lc_rope_hi(k1, k0, c, sn));
-        dot = fmaf(static_cast<float>(qr), static_cast<float>(kr[e]), dot);
+        dot = fmaf(qok ? static_cast<float>(qr) : 0.f, static_cast<float>(kr[e]), dot);
         v_new[j][e] = static_cast<float>(xv[e]);
       }
 #pragma unroll
@@ -967,11 +1003,18 @@ int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, f
   const unsigned threads = 64 * cluster_waves<DPAD>();
   T* o = static_cast<T*>(out);
   const StepArgs none{};
-  if (a.bias != nullptr)
-    paged_decode_cluster_kernel<T, DPAD, true, false>
+  const bool pre = a.max_pages <= 64;
+  if (a.bias != nullptr && pre)
+    paged_decode_cluster_kernel<T, DPAD, true, false, true>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
+  else if (a.bias != nullptr)
+    paged_decode_cluster_kernel<T, DPAD, true, false, false>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
+  else if (pre)
+    paged_decode_cluster_kernel<T, DPAD, false, false, true>
         <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
   else
-    paged_decode_cluster_kernel<T, DPAD, false, false>
+    paged_decode_cluster_kernel<T, DPAD, false, false, false>
         <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
   return lc_check_launch("lc_paged_decode_fwd (single split)");
 }
@@ -982,11 +1025,18 @@ int launch_step(const DecodeArgs& a, const StepArgs& sa, void* out, int64_t o_sb
   dim3 grid(a.Hkv * a.n_hgroups, a.B);
   const unsigned threads = 64 * cluster_waves<DPAD>();
   T* o = static_cast<T*>(out);
-  if (a.bias != nullptr)
-    paged_decode_cluster_kernel<T, DPAD, true, true>
+  const bool pre = a.max_pages <= 64;
+  if (a.bias != nullptr && pre)
+    paged_decode_cluster_kernel<T, DPAD, true, true, true>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, sa);
+  else if (a.bias != nullptr)
+    paged_decode_cluster_kernel<T, DPAD, true, true, false>
+        <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, sa);
+  else if (pre)
+    paged_decode_cluster_kernel<T, DPAD, false, true, true>
         <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, sa);
   else
-    paged_decode_cluster_kernel<T, DPAD, false, true>
+    paged_decode_cluster_kernel<T, DPAD, false, true, false>
         <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, sa);
   return lc_check_launch("lc_paged_decode_step");
 }
