@@ -75,9 +75,18 @@ def decode_bytes(lens, B, Hq, Hkv, D, P):
     return kv + B * Hq * D * 2 * 2 + B * Hq * 4 + sum(math.ceil(n / P) for n in lens) * 4 + B * 4
 
 
-def time_steps(fn, steps, warmup):
+def time_steps(fn, steps, warmup, ramp_ms=250.0):
+    """Times `steps` calls of fn after `warmup` untimed ones. Before those, fn
+    runs untimed for at least ramp_ms of wall time: the GPU's clocks take
+    ~100 ms of load to settle (config 2 measured 203 us per call over 20 steps
+    right after start, 195 us after the ramp). Returns (ms per step from
+    events on the current stream, host wall ms per step)."""
     import torch
 
+    t_ramp = time.perf_counter()
+    while (time.perf_counter() - t_ramp) * 1e3 < ramp_ms:
+        fn()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -154,7 +163,7 @@ def run_decode(args, shape):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_rows_kernel + decode_merge_kernel (one decode call)",
+            "kernel": "paged decode split kernel + decode_merge_kernel (one decode call)",
             "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

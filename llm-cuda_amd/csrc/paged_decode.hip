@@ -263,15 +263,16 @@ __device__ __forceinline__ void load_q(const DecodeArgs& a, int b, int h, int h_
 // first step's K/V loads are issued (a place for arithmetic on the loaded
 // operands that should not hold up that issue). HB: the call carries an
 // additive bias (loaded with the step's K/V, one step ahead).
-// PRE: the caller has loaded the sequence's whole block-table row (max_pages
-// <= 64; entry `lane` per lane, -1 past the row) and passes it as row_entry,
-// so no table load is issued here.
+// PRE: the caller has loaded a 64-page window of the sequence's block-table
+// row that covers the range (entry window_base + lane per lane, -1 past the
+// row) and passes it as row_entry, so no table load is issued here.
 template <typename T, int DPAD, bool HB, bool PRE = false, typename QLoad, typename QFinish>
 __device__ __forceinline__ void rows_range(const DecodeArgs& a, int b, int kvh, int h,
                                            bool head_ok, int t_begin, int t_end, QLoad load_q,
                                            QFinish finish_q, T* lds_k, T* lds_v,
                                            f32x4_t (&o)[DPAD / 16], float& m_ref,
-                                           float& l_lane, int row_entry = -2) {
+                                           float& l_lane, int row_entry = -2,
+                                           int window_base = 0) {
   typedef MfmaOps<T> Ops;
   typedef typename Ops::v8 v8;
   constexpr int KS = DPAD / 32;      // MFMA k-steps over head_dim
@@ -289,7 +290,8 @@ __device__ __forceinline__ void rows_range(const DecodeArgs& a, int b, int kvh, 
   const bool chunk_in_d = schunk * 8 < a.D;
 
   // Block-table entries of this range, one per lane (or the preloaded row).
-  const int first_page = PRE ? 0 : (a.p_shift >= 0 ? (t_begin >> a.p_shift) : (t_begin / a.P));
+  const int first_page =
+      PRE ? window_base : (a.p_shift >= 0 ? (t_begin >> a.p_shift) : (t_begin / a.P));
   const int last_page = a.p_shift >= 0 ? ((t_end - 1) >> a.p_shift) : ((t_end - 1) / a.P);
   int my_page = row_entry;
   if constexpr (!PRE)
@@ -499,23 +501,34 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   const int hg = blockIdx.x - kvh * a.n_hgroups;
   const int b = blockIdx.y;
   const int cap = a.max_pages * a.P;
-  // PRE (max_pages <= 64): the block-table row is loaded whole (one entry per
-  // lane) together with the length, so the first K/V loads wait on one round
-  // trip, not on the length and then the table.
+  // This workgroup's split: tokens [s_begin, s_begin + split_tokens).
+  const int split = blockIdx.z;
+  const int s_begin = split * a.split_tokens;
+  // PRE (the split's pages fit 64 block-table entries): the window of the row
+  // from the split's first page is loaded whole (one entry per lane) together
+  // with the length, so the first K/V loads wait on one round trip, not on
+  // the length and then the table.
+  const int window_base = a.p_shift >= 0 ? (s_begin >> a.p_shift) : (s_begin / a.P);
   int row_entry = -1;
-  if constexpr (PRE) row_entry = a.bt[(int64_t)b * a.bt_stride + min(lane, a.max_pages - 1)];
+  if constexpr (PRE)
+    row_entry = a.bt[(int64_t)b * a.bt_stride + min(window_base + lane, a.max_pages - 1)];
   const int p_new = STEP ? a.seq_lens[b] : 0;  // the new token's position
   const int len = STEP ? min(max(p_new, 0), cap) : seq_len_of(a, b);
   if constexpr (PRE) {
-    row_entry = lane < a.max_pages ? row_entry : -1;
+    row_entry = window_base + lane < a.max_pages ? row_entry : -1;
     // Keep the row load here, beside the length's, rather than sunk to its use.
     asm volatile("" : "+v"(row_entry));
   }
+  // With several splits, a split past the length writes nothing (the merge
+  // reads only the splits that hold tokens); a single split always writes the
+  // output (zeros for an empty sequence).
+  if (a.max_splits > 1 && s_begin >= len) return;
   const int prow = p_new < 0 ? 0 : min(p_new, sa.table_rows - 1);
   const int half = a.D / 2;
-  const int nsteps = (len + kStep - 1) / kStep;
-  const int t_begin = (wave * nsteps / W) * kStep;
-  const int t_end = min(len, ((wave + 1) * nsteps / W) * kStep);
+  const int s_len = min(len - s_begin, a.split_tokens);
+  const int nsteps = s_len > 0 ? (s_len + kStep - 1) / kStep : 0;
+  const int t_begin = s_begin + (wave * nsteps / W) * kStep;
+  const int t_end = min(len, s_begin + ((wave + 1) * nsteps / W) * kStep);
 
   const int col = lane & 15;
   const int q4 = lane >> 4;
@@ -533,7 +546,7 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   if constexpr (STEP) {
     const int pc = p_new >= 0 && p_new < cap ? p_new : 0;
     const int pi = a.p_shift >= 0 ? (pc >> a.p_shift) : (pc / a.P);
-    if constexpr (PRE)
+    if constexpr (PRE)  // single split: the window starts at page 0
       nt_phys = __builtin_amdgcn_readlane(row_entry, pi);
     else
       nt_phys = a.bt[(int64_t)b * a.bt_stride + pi];
@@ -609,12 +622,12 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
               }
             }
           },
-          my_k, my_v, o, m_ref, l_lane, row_entry);
+          my_k, my_v, o, m_ref, l_lane, row_entry, window_base);
     } else {
       rows_range<T, DPAD, HB, PRE>(
           a, b, kvh, h, head_ok, t_begin, t_end,
           [&](v8 (&qop)[KS]) { load_q<T, DPAD>(a, b, h, kvh * a.G, head_ok, q4, qop); },
-          [](v8 (&)[KS]) {}, my_k, my_v, o, m_ref, l_lane, row_entry);
+          [](v8 (&)[KS]) {}, my_k, my_v, o, m_ref, l_lane, row_entry, window_base);
     }
   }
 
@@ -721,6 +734,16 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
     }
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     const int hh = kvh * a.G + gg;
+    if (a.max_splits > 1) {
+      // The split's normalised partial and log2-domain lse, for the merge.
+      const int64_t pidx = ((int64_t)b * a.Hq + hh) * a.max_splits + split;
+      f32x4_t w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = acc[i] * inv;
+      *reinterpret_cast<f32x4_t*>(a.part_o + pidx * a.D + d0) = w;
+      if (d0 == 0) a.part_lse[pidx] = lsum > 0.f ? mx + lc_log2(lsum) : -INFINITY;
+      continue;
+    }
     T* oh = out + (int64_t)b * o_sb + (int64_t)hh * o_sh + d0;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -999,11 +1022,15 @@ int launch_merge(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, flo
 template <typename T, int DPAD>
 int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, float* lse,
                    hipStream_t st) {
-  dim3 grid(a.Hkv * a.n_hgroups, a.B);
+  // Split-major order (blockIdx.z = split), as in the one-wave kernel.
+  dim3 grid(a.Hkv * a.n_hgroups, a.B, a.max_splits);
   const unsigned threads = 64 * cluster_waves<DPAD>();
   T* o = static_cast<T*>(out);
   const StepArgs none{};
-  const bool pre = a.max_pages <= 64;
+  // A split starting at any multiple of split_tokens touches at most
+  // (split_tokens - 1) / P + 2 pages; one split reads pages 0 .. max_pages-1.
+  const bool pre = a.max_splits == 1 ? a.max_pages <= 64
+                                     : (a.split_tokens - 1) / a.P + 2 <= 64;
   if (a.bias != nullptr && pre)
     paged_decode_cluster_kernel<T, DPAD, true, false, true>
         <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
@@ -1016,7 +1043,9 @@ int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, f
   else
     paged_decode_cluster_kernel<T, DPAD, false, false, false>
         <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
-  return lc_check_launch("lc_paged_decode_fwd (single split)");
+  const int rc = lc_check_launch("lc_paged_decode_fwd (workgroup splits)");
+  if (rc != LC_OK || a.max_splits == 1) return rc;
+  return launch_merge<T>(a, out, o_sb, o_sh, lse, st);
 }
 
 template <typename T, int DPAD>
@@ -1170,13 +1199,21 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
   const bool row_pages = page_size % 32 == 0 &&
                          ((page_size - 1) * kv_s_tok + D) * esz < (1LL << 31);
   const bool rows = row_pages && (split_tokens - 1) / page_size + 2 <= 64;
-  // Single split (one workgroup of W waves per sequence and head group): every
-  // wave's share of the capacity, whole 32-token steps starting on a step
-  // boundary, must fit the row kernel's 64 block-table entries.
+  // Workgroup splits (one workgroup of W waves per split, the split's steps
+  // shared among its waves and merged in LDS) are taken for a single split,
+  // for splits of >= 2048 tokens, and when the grid has <= 512 splits (one-wave
+  // splits would leave most of the CUs' wave slots empty). Measured against
+  // one wave per split: config 2 192 us at 2048-token splits against 197 us
+  // at 512; 1024-token splits were 2-5% slower in workgroups on the ragged
+  // shapes tried. Every wave's share, whole 32-token steps starting on a step
+  // boundary, must fit the row kernel's 64 table entries.
   const int64_t waves = D <= 128 ? cluster_waves<128>() : cluster_waves<256>();
-  const int64_t cap_steps = (max_pages_per_seq * page_size + kStep - 1) / kStep;
-  const int64_t wave_tokens = (cap_steps + waves - 1) / waves * kStep;
-  const bool cluster = row_pages && max_splits == 1 && (wave_tokens - 1) / page_size + 2 <= 64;
+  const int64_t span = max_splits == 1 ? max_pages_per_seq * page_size : split_tokens;
+  const int64_t wave_tokens = ((span + kStep - 1) / kStep + waves - 1) / waves * kStep;
+  const int64_t units = B * Hkv * ((Hq / Hkv + 15) / 16);
+  const bool cluster = row_pages &&
+                       (max_splits == 1 || split_tokens >= 2048 || units * max_splits <= 512) &&
+                       (wave_tokens - 1) / page_size + 2 <= 64;
   hipStream_t st = lc_stream(stream);
   switch (dtype) {
     case LC_DTYPE_F32:

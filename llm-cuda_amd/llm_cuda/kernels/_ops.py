@@ -453,60 +453,85 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
 # Paged decode  (reference: kernels/triton/decode_attention.py:204-287 over
 # models/llama3/kv_cache.py:65-83)
 # ---------------------------------------------------------------------------
-def single_split_fits(capacity_tokens: int, page_size: int, head_dim: int) -> bool:
-    """Whether one split covering the capacity runs the single-split kernel
-    (one workgroup of 8 waves, 4 above head_dim 128, per sequence and head
-    group): pages of a multiple of 32 tokens, and every wave's share of the
-    capacity's 32-token steps within 64 pages."""
-    if page_size % 32 != 0:
-        return False
-    waves = 8 if head_dim <= 128 else 4
-    steps = -(-capacity_tokens // 32)
-    wave_tokens = -(-steps // waves) * 32
+def _workgroup_waves(head_dim: int) -> int:
+    return 8 if head_dim <= 128 else 4
+
+
+def _wave_window_fits(span_tokens: int, page_size: int, head_dim: int) -> bool:
+    """Whether each workgroup wave's share of span_tokens (whole 32-token steps
+    from a step boundary) touches at most 64 pages (one table entry per lane)."""
+    waves = _workgroup_waves(head_dim)
+    wave_tokens = -(-(-(-span_tokens // 32)) // waves) * 32
     return (wave_tokens - 1) // page_size + 2 <= 64
+
+
+def single_split_fits(capacity_tokens: int, page_size: int, head_dim: int) -> bool:
+    """Whether one split covering the capacity runs the workgroup kernel (8
+    waves, 4 above head_dim 128, per sequence and head group): pages of a
+    multiple of 32 tokens, and every wave's share of the capacity's 32-token
+    steps within 64 pages."""
+    return page_size % 32 == 0 and _wave_window_fits(capacity_tokens, page_size, head_dim)
+
+
+def takes_workgroup_splits(units: int, split_tokens: int, max_splits: int, page_size: int,
+                           head_dim: int, capacity_tokens: int) -> bool:
+    """The library's choice between one workgroup per split and one wave per
+    split (mirrors lc_paged_decode_fwd): workgroups for a single split, splits
+    of >= 2048 tokens, or grids of <= 512 splits."""
+    span = capacity_tokens if max_splits == 1 else split_tokens
+    return (page_size % 32 == 0 and _wave_window_fits(span, page_size, head_dim)
+            and (max_splits == 1 or split_tokens >= 2048 or units * max_splits <= 512))
 
 
 def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens: int,
                         page_size: int = 64, head_dim: int = 128,
-                        uniform_lengths: bool = False, n_cus: int = 256) -> int:
-    """Tokens per split-K wave.
+                        uniform_length: int | None = None, n_cus: int = 256) -> int:
+    """Tokens per split.
 
-    With uniform_lengths (every sequence of the batch equally long, as in a
-    batched decode step) and units filling whole rounds of the CUs, one split
-    covers the capacity: the single-split kernel gives each unit one
-    workgroup whose waves share its tokens evenly and merge in LDS, with no
-    partials and no merge kernel (config 4: 43.6 us against 46.0 us for
-    512-token splits; 82.7 against 85.3 at 4096 tokens). It is kept off
-    ragged batches, where the longest sequence would set every unit's time.
-
-    Each split pays a fixed cost (its first dependent loads, its partial output
-    and its share of the merge) and a ragged batch ends in a tail of splits, so
-    the split size trades those against filling the 256 CUs. Measured on the
-    benchmark shapes (one wave per split, ~8 resident per CU):
-      * many (sequence, kv head) units (>= 256: config 2's 512, config 4's 256):
-        512-token splits; 256 was 3% slower at config 4 and larger splits lose
-        to the ragged tail at config 2;
-      * few units (config 5's 64 at 32K tokens): the largest of 2048 / 1024 /
-        512 that still gives >= 1024 splits (2048: 169 us against 186 us at 512);
-      * if even 512 leaves fewer than 1024 splits, halve down to 64.
-    Splits above 512 are used only where the row kernel (pages of a multiple
-    of 32 tokens, at most 64 pages per split) still takes them.
+    units = batch x kv heads x groups of <= 16 query heads. Where the page
+    size allows workgroup splits (a multiple of 32 tokens):
+      * uniform_length given (every sequence holds that many tokens, as in a
+        batched decode step): the fewest splits per unit s whose units * s
+        fill whole rounds of the CUs to >= 90%, each split a 1/s share of the
+        length; s = 1 is one split over the capacity. Measured: config 4
+        (256 units) 43.6 us against 46.0 us for 512-token splits; config 5
+        (64 units x 4 splits of 8256) 168.9 us against 174.8 us at 2048.
+      * lengths unknown (ragged): about 8 splits per CU for >= 256 units
+        (config 2: 2048-token splits, 192 us against 197 us at 512), one round
+        of the CUs for fewer units (16 sequences of 1-16K tokens, 128 units:
+        115.7 us at 8192 against 127-133 us at 512-2048).
+    Where the library would run such a split size with one wave per split
+    instead (see takes_workgroup_splits), or pages are not a multiple of 32,
+    one-wave splits: 512 tokens, shrunk until there are >= 1024 of them.
     """
     units = batch * n_kv_heads * ((group + 15) // 16)
-    if (uniform_lengths and units >= n_cus and units % n_cus == 0
-            and single_split_fits(capacity_tokens, page_size, head_dim)):
-        return -(-capacity_tokens // 64) * 64
-    rows_cap = 62 * page_size + 1 if page_size % 32 == 0 else 512
+    if page_size % 32 == 0 and capacity_tokens > 0:
+        if uniform_length is not None:
+            length = max(1, min(int(uniform_length), capacity_tokens))
+            s = 1
+            while s < 64:
+                n = units * s
+                if n >= n_cus and n / (n_cus * -(-n // n_cus)) >= 0.9:
+                    break
+                s += 1
+            split = -(-(-(-length // s)) // 64) * 64
+        elif units >= n_cus:
+            s = -(-8 * n_cus // units)
+            split = -(-(-(-capacity_tokens // s)) // 64) * 64
+        else:
+            s = max(1, n_cus // units)
+            split = -(-(-(-capacity_tokens // s)) // 64) * 64
+        if s == 1 or split >= capacity_tokens:
+            split = -(-capacity_tokens // 64) * 64
+        max_splits = -(-capacity_tokens // split)
+        if takes_workgroup_splits(units, split, max_splits, page_size, head_dim,
+                                  capacity_tokens):
+            return split
 
     def n_splits(split: int) -> int:
         return units * ((capacity_tokens + split - 1) // split)
 
     split = 512
-    if units < 256:
-        for big in (2048, 1024):
-            if big <= rows_cap and n_splits(big) >= 1024:
-                split = big
-                break
     while split > 64 and n_splits(split) < 1024:
         split //= 2
     return split
@@ -516,19 +541,19 @@ def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Te
                  block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None = None,
                  return_lse: bool = False, split_tokens: int | None = None,
                  workspace: torch.Tensor | None = None,
-                 attention_mask: torch.Tensor | None = None, uniform_lengths: bool = False):
+                 attention_mask: torch.Tensor | None = None, uniform_length: int | None = None):
     """One-token GQA attention per sequence over a paged K/V pool (forward only).
 
     q: [B, Hq, 1, D] or [B, Hq, D]; key_pages, value_pages: [N, Hkv, P, D];
     block_table: int32 [B, max_pages]; seq_lens: int32 [B]. attention_mask:
     additive scores for the query token, broadcastable to [B, Hq, 1, L] (or
     [B, Hq, L]); token t < L of a sequence gets mask[..., t], later tokens
-    none. uniform_lengths: the caller knows every seq_lens entry is equal (a
-    hint for the split choice only; results do not depend on it). Returns out
-    with q's shape (and lse [B, Hq] fp32 if return_lse).
+    none. uniform_length: every seq_lens entry is known to equal this (a hint
+    for the split choice only; results do not depend on it). Returns out with
+    q's shape (and lse [B, Hq] fp32 if return_lse).
     """
     args = (block_table, seq_lens, scale, return_lse, split_tokens, workspace, attention_mask,
-            uniform_lengths)
+            uniform_length)
     if _records_grad(q, key_pages, value_pages):
         return _ForwardOnly.apply("paged_decode", lambda a, k, v: _paged_decode(a, k, v, *args),
                                   q, key_pages, value_pages)
@@ -538,7 +563,7 @@ def paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Te
 def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
                   block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float | None,
                   return_lse: bool, split_tokens: int | None, workspace: torch.Tensor | None,
-                  attention_mask: torch.Tensor | None = None, uniform_lengths: bool = False):
+                  attention_mask: torch.Tensor | None = None, uniform_length: int | None = None):
     squeeze = q.dim() == 3
     q4 = q.unsqueeze(2) if squeeze else q
     if q4.dim() != 4 or q4.shape[2] != 1:
@@ -574,7 +599,7 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
     capacity = maxp * P
     G = Hq // Hkv
     if split_tokens is None:
-        split_tokens = choose_split_tokens(B, Hkv, G, capacity, P, D, uniform_lengths,
+        split_tokens = choose_split_tokens(B, Hkv, G, capacity, P, D, uniform_length,
                                            _cu_count(dev))
     max_splits = max(1, (capacity + split_tokens - 1) // split_tokens)
     if scale is None:

@@ -95,7 +95,7 @@ def triton_decode_attention(
     pages_v = v.as_strided((B, Hkv, L, D), v.stride())
     table, lens = _identity_table(B, L, q.device)
     return _ops.paged_decode(q, pages_k, pages_v, table, lens, return_lse=return_lse,
-                             uniform_lengths=True)
+                             uniform_length=L)
 
 
 def paged_decode_attention(
@@ -109,14 +109,14 @@ def paged_decode_attention(
     split_tokens: int | None = None,
     workspace: torch.Tensor | None = None,
     attention_mask: torch.Tensor | None = None,
-    uniform_lengths: bool = False,
+    uniform_length: int | None = None,
 ):
     """attention_mask: the reference's additive mask for the query token,
     broadcastable to [B, Hq, 1, L]; token t < L of each sequence gets
     mask[..., t] added to its scaled score (models/llama3/attention.py:85-86),
-    later tokens none. uniform_lengths: every seq_lens entry is known to be
-    equal (a split-choice hint; the result does not depend on it)."""
+    later tokens none. uniform_length: every seq_lens entry is known to equal
+    this (a split-choice hint; the result does not depend on it)."""
     return _ops.paged_decode(q, key_pages, value_pages, block_table, seq_lens, scale=scale,
                              return_lse=return_lse, split_tokens=split_tokens,
                              workspace=workspace, attention_mask=attention_mask,
-                             uniform_lengths=uniform_lengths)
+                             uniform_length=uniform_length)

@@ -149,7 +149,7 @@ class Llama3Attention(nn.Module):
                 q = cache.append_rotated(q, k, v, cos_t, sin_t)
                 out = paged_decode_attention(
                     q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens,
-                    attention_mask=attention_mask, uniform_lengths=cache.uniform_lengths)
+                    attention_mask=attention_mask, uniform_length=cache.uniform_length)
             out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
             return self.o_proj(out), cache
 
@@ -171,7 +171,7 @@ class Llama3Attention(nn.Module):
                     raise ValueError("decode step against an empty cache")
                 out = paged_decode_attention(
                     q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens,
-                    attention_mask=mask, uniform_lengths=cache.uniform_lengths)
+                    attention_mask=mask, uniform_length=cache.uniform_length)
             elif use_cache and past_len == 0:
                 out = triton_fused_causal_attention(q, k, v, attention_mask=mask)
             else:

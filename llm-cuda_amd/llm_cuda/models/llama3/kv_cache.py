@@ -93,9 +93,11 @@ class PagedKVLayerCache:
         return first
 
     @property
-    def uniform_lengths(self) -> bool:
-        """Whether every sequence holds the same number of tokens (host mirror)."""
-        return all(n == self.lengths[0] for n in self.lengths)
+    def uniform_length(self) -> int | None:
+        """The common number of cached tokens when every sequence holds the
+        same number (host mirror), else None."""
+        first = self.lengths[0]
+        return first if all(n == first for n in self.lengths) else None
 
     def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
         if k.shape != v.shape:
@@ -143,13 +145,14 @@ class PagedKVLayerCache:
         CUs, and sizes the fused kernel supports (its single split must be
         the split the decode heuristic would choose)."""
         capacity = self.max_pages * self.page_size
-        if not (self.uniform_lengths and self.key_pages.is_cuda
+        length = self.uniform_length
+        if not (length is not None and self.key_pages.is_cuda
                 and _ops.decode_step_supported(dtype, self.head_dim, self.page_size, capacity)):
             return False
         group = n_heads // self.num_kv_heads
         split = _ops.choose_split_tokens(
             self.batch_size, self.num_kv_heads, group, capacity, self.page_size, self.head_dim,
-            True, _ops._cu_count(self.key_pages.device))
+            length + 1, _ops._cu_count(self.key_pages.device))
         return split >= capacity
 
     def decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,

@@ -183,31 +183,33 @@ def test_kv_cache_argument_checks():
 
 
 def test_split_heuristic():
-    from llm_cuda.kernels._ops import choose_split_tokens
+    from llm_cuda.kernels._ops import choose_split_tokens, takes_workgroup_splits
 
-    # config 2 (64 ragged sequences) and config 4 (32 at 2K tokens): 512-token splits
-    assert choose_split_tokens(64, 8, 4, 8192) == 512
+    # config 2 (64 ragged sequences, 512 units, capacity 8000): 2048-token
+    # workgroup splits, about 8 per CU
+    assert choose_split_tokens(64, 8, 4, 8000) == 2048
+    assert takes_workgroup_splits(512, 2048, 4, 64, 128, 8000)
+    # config 4 (32 sequences at 2049 tokens, 256 units): one split over the
+    # capacity when the common length is known, 512-token one-wave splits when not
+    assert choose_split_tokens(32, 8, 4, 2112, 64, 128, 2049) == 2112
     assert choose_split_tokens(32, 8, 4, 2112) == 512
-    # config 5 (8 sequences of 32K tokens, 64 units): 2048-token splits
-    assert choose_split_tokens(8, 8, 8, 32768) == 2048
-    # tiny batch: splits shrink to keep the grid busy, never below 64.
-    assert choose_split_tokens(1, 2, 4, 128) == 64
-    for args in [(1, 1, 1, 1), (3, 5, 7, 1000), (64, 8, 16, 100000)]:
+    assert not takes_workgroup_splits(256, 512, 5, 64, 128, 2112)
+    # config 5 (8 sequences of 32K tokens, 64 units): 4 splits per unit, one
+    # round of the CUs, known length or not
+    assert choose_split_tokens(8, 8, 8, 32768) == 8192
+    assert choose_split_tokens(8, 8, 8, 32768, 64, 128, 32768) == 8192
+    # one sequence of 32K tokens (8 units): 32 splits, small grid -> workgroups
+    assert choose_split_tokens(1, 8, 4, 32832) == 1088
+    assert takes_workgroup_splits(8, 1088, 31, 64, 128, 32832)
+    # equal lengths: the fewest splits per unit that fill rounds of the CUs
+    assert choose_split_tokens(64, 8, 4, 4160, 64, 128, 4096) == 4160  # 512 units, 1 split
+    assert choose_split_tokens(48, 8, 4, 8192, 64, 128, 8000) == 4032  # 384 units, 2 splits
+    # pages of 48 tokens: one-wave splits only
+    assert choose_split_tokens(64, 8, 4, 8000, 48) == 512
+    assert choose_split_tokens(1, 2, 4, 128, 48) == 64
+    for args in [(1, 1, 1, 1), (3, 5, 7, 1000), (64, 8, 16, 100000), (2, 8, 8, 65536)]:
         s = choose_split_tokens(*args)
-        assert s % 64 == 0 and 64 <= s <= 2048
-    # uniform lengths with whole rounds of 256 units: one split over the capacity
-    assert choose_split_tokens(32, 8, 4, 2112, 64, 128, True) == 2112
-    assert choose_split_tokens(64, 8, 4, 4160, 64, 128, True) == 4160
-    assert choose_split_tokens(32, 8, 4, 2100, 64, 128, True) == 2112  # rounded up to 64
-    # ... but not for 384 units (1.5 rounds), 128 units, pages of 48 tokens, or
-    # a capacity whose per-wave share exceeds 64 pages (8 waves x 62 pages)
-    assert choose_split_tokens(48, 8, 4, 2112, 64, 128, True) == 512
-    assert choose_split_tokens(16, 8, 4, 2112, 64, 128, True) < 2112
-    assert choose_split_tokens(32, 8, 4, 2112, 48, 128, True) == 512
-    assert choose_split_tokens(32, 8, 4, 40000, 64, 128, True) == 512
-    # head_dim 256 runs 4 waves per workgroup: half the capacity fits
-    assert choose_split_tokens(32, 8, 4, 16384, 64, 128, True) == 16384
-    assert choose_split_tokens(32, 8, 4, 16384, 64, 256, True) == 512
+        assert s % 64 == 0 and s >= 64
 
 
 def test_single_split_fit_matches_the_library_rule():
