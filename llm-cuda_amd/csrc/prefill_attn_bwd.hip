@@ -316,6 +316,10 @@ constexpr int kBwRows = 32;   // dQ kernel: query rows per wave
 constexpr int kBwTile = 64;   // rows per LDS tile (keys for dQ, queries for dK/dV)
 constexpr int kBkWaves = 4;             // dK/dV kernel: waves per workgroup (32 keys each)
 constexpr int kBkKeys = 32 * kBkWaves;  // keys per dK/dV workgroup
+// Depth of the dK/dV pipeline's LDS operand ring (MFMA slots read ahead).
+constexpr int kBkRing = 8;
+// Mask selector for the dK/dV loop: decide per tile at run time.
+constexpr int kRuntimeMask = 2;
 
 // LDS offsets shared by both kernels for a tile of 64 rows x DPAD.
 template <int DPAD, int T_SIZE>
@@ -616,9 +620,23 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
 //   dK^T += Q^T dS   (A: transposed reads of the Q tile, B: dS)
 // Q, dO, lse2 and delta tiles are double-buffered in LDS, fetched by DMA one
 // tile ahead. Blocks are dispatched heaviest (earliest keys) first.
+//
+// Without a bias the tile runs as one software pipeline of four phases of
+// 2 DPAD/16 MFMA slots each (16 at D 128; one wave per SIMD, so the schedule
+// itself has to hide every latency):
+//   phase 0  S, dP of query rows 0-31
+//   phase 1  S, dP of rows 32-63, with the softmax of rows 0-31
+//   phase 2  dV, dK of rows 0-31, with the softmax of rows 32-63
+//   phase 3  dV, dK of rows 32-63
+// and the LDS operand of slot i read at slot i - kBkRing into a register
+// ring; scheduling fences pin the order so the compiler cannot pull the
+// reads back next to their MFMAs. Unmasked and diagonal tiles run in two
+// separate loops so that no tile body holds a branch.
 // ---------------------------------------------------------------------------
 // BIAS: 0 none, 1 = dtype T, 2 = fp32. Queries sit on accumulator rows here,
-// so a lane's bias values (one key, 32 query rows) are read one element each.
+// so a lane's bias values (one key, 32 query rows) are read one element each;
+// bias tiles keep the plain phase order (the 32 bias registers do not fit the
+// pipeline's budget).
 template <typename T, int DPAD, int BIAS>
 __global__ __launch_bounds__(64 * kBkWaves) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 attn_bwd_dkv_mfma_kernel(BwdArgs a) {
@@ -649,7 +667,10 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a) {
   const int unit = blockIdx.x - kb * n_units;
   const int kvh = unit % a.Hkv;
   const int b = unit / a.Hkv;
-  const int key0 = kb * kBkKeys + wave * 32;  // this wave's first key
+  // This wave's first key. The pipelined path needs it wave-uniform (scalar
+  // branches around branch-free tiles); the bias path keeps the per-lane copy,
+  // with which its tiles allocate without spilling.
+  const int key0 = kb * kBkKeys + (BIAS == 0 ? wave_s : wave) * 32;
   const int kj = key0 + l32;
   const bool key_ok = kj < a.Skv;
 
@@ -762,88 +783,195 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a) {
     LC_LDS const char* ol = obuf(p_c);
     LC_LDS const float* ll = lbuf(p_c);
     LC_LDS const float* dl = dbuf(p_c);
-    f32x16_t sa[2], dpa[2];
+    if constexpr (BIAS != 0) {
+      f32x16_t sa[2], dpa[2];
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
+      for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sa[h2][r] = 0.f;
-        dpa[h2][r] = 0.f;
-      }
+        for (int r = 0; r < 16; ++r) {
+          sa[h2][r] = 0.f;
+          dpa[h2][r] = 0.f;
+        }
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+      for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        sa[h2] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(ql + ad.row[s] + h2 * 32 * ROW_B),
-                          kop[s], sa[h2]);
-        dpa[h2] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(ol + ad.row[s] + h2 * 32 * ROW_B),
-                           vop[s], dpa[h2]);
-      }
-    v8 pop[2][2], dsop[2][2];
+        for (int h2 = 0; h2 < 2; ++h2) {
+          sa[h2] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(ql + ad.row[s] + h2 * 32 * ROW_B),
+                            kop[s], sa[h2]);
+          dpa[h2] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(ol + ad.row[s] + h2 * 32 * ROW_B),
+                             vop[s], dpa[h2]);
+        }
+      v8 pop[2][2], dsop[2][2];
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
+      for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = h2 * 32 + j * 8 + hh * 4;
-        const f32x4_t l4 = *reinterpret_cast<LC_LDS const f32x4_t*>(ll + row);
-        const f32x4_t d4 = *reinterpret_cast<LC_LDS const f32x4_t*>(dl + row);
+        for (int j = 0; j < 4; ++j) {
+          const int row = h2 * 32 + j * 8 + hh * 4;
+          const f32x4_t l4 = *reinterpret_cast<LC_LDS const f32x4_t*>(ll + row);
+          const f32x4_t d4 = *reinterpret_cast<LC_LDS const f32x4_t*>(dl + row);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = j * 4 + i;
-          float x = fmaf(sa[h2][r], a.scale_log2, -l4[i]);
-          if constexpr (BIAS != 0) x += lc_bias_log2(bv[h2][r]);
-          if constexpr (decltype(mask_c)::value) {
-            if (kj > qt * kBwTile + row + i + a.q_offset) x = -INFINITY;
+          for (int i = 0; i < 4; ++i) {
+            const int r = j * 4 + i;
+            float x = fmaf(sa[h2][r], a.scale_log2, -l4[i]);
+            x += lc_bias_log2(bv[h2][r]);
+            if constexpr (decltype(mask_c)::value) {
+              if (kj > qt * kBwTile + row + i + a.q_offset) x = -INFINITY;
+            }
+            const float p = lc_exp2(x);
+            pop[h2][r >> 3][r & 7] = static_cast<T>(p);
+            dsop[h2][r >> 3][r & 7] = static_cast<T>(p * (dpa[h2][r] - d4[i]));
           }
-          const float p = lc_exp2(x);
-          pop[h2][r >> 3][r & 7] = static_cast<T>(p);
-          dsop[h2][r >> 3][r & 7] = static_cast<T>(p * (dpa[h2][r] - d4[i]));
+        }
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+          for (int dt = 0; dt < DTL; ++dt) {
+            const int rowoff = (h2 * 32 + jp * 16) * ROW_B;
+            const i16x4_t olo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (LC_LDS i16x4_t*)(ol + ad.tr[0][dt] + rowoff));
+            const i16x4_t ohi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (LC_LDS i16x4_t*)(ol + ad.tr[1][dt] + rowoff));
+            dv[dt] = Ops::mma(__builtin_bit_cast(v8, __builtin_shufflevector(olo, ohi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                              pop[h2][jp], dv[dt]);
+            const i16x4_t qlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (LC_LDS i16x4_t*)(ql + ad.tr[0][dt] + rowoff));
+            const i16x4_t qhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (LC_LDS i16x4_t*)(ql + ad.tr[1][dt] + rowoff));
+            dk[dt] = Ops::mma(__builtin_bit_cast(v8, __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                              dsop[h2][jp], dk[dt]);
+          }
+    } else {
+      // S/dP accumulators of both 32-row halves, P and dS operands.
+      f32x16_t acc_s[2], acc_p[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          acc_s[x][r] = 0.f;
+          acc_p[x][r] = 0.f;
+        }
+      v8 pop[2][2], dsop[2][2];
+      f32x4_t l4[2][4], d4[2][4];
+      auto read_rows = [&](int h2) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = h2 * 32 + j * 8 + hh * 4;
+          l4[h2][j] = *reinterpret_cast<LC_LDS const f32x4_t*>(ll + row);
+          d4[h2][j] = *reinterpret_cast<LC_LDS const f32x4_t*>(dl + row);
+        }
+      };
+      // NPH MFMA slots per phase (2 KS for S/dP of a half = 4 DTL for its
+      // dV/dK); EPS softmax elements per slot.
+      constexpr int NPH = 2 * KS, EPS = 16 / NPH;
+      static_assert(4 * DTL == NPH && NPH * EPS == 16, "slot table");
+      // LDS operand of slot i: Q/dO rows for S/dP (even slot Q, odd dO),
+      // transposed dO/Q for dV/dK (even slot dO, odd Q).
+      auto operand = [&](int i) __attribute__((always_inline)) -> v8 {
+        if (i < 2 * NPH) {
+          const int h2 = i / NPH, s = (i % NPH) >> 1;
+          LC_LDS const char* base = (i & 1) ? ol : ql;
+          return *reinterpret_cast<LC_LDS const v8*>(base + ad.row[s] + h2 * 32 * ROW_B);
+        }
+        const int k = i - 2 * NPH;
+        const int h2 = k / NPH, jp = (k % NPH) / (2 * DTL), dt = (k % (2 * DTL)) >> 1;
+        LC_LDS const char* base = (k & 1) ? ql : ol;
+        const int rowoff = (h2 * 32 + jp * 16) * ROW_B;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(base + ad.tr[0][dt] + rowoff));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LC_LDS i16x4_t*)(base + ad.tr[1][dt] + rowoff));
+        return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      };
+      auto mfma = [&](int i, const v8& A) __attribute__((always_inline)) {
+        if (i < 2 * NPH) {
+          const int h2 = i / NPH, s = (i % NPH) >> 1;
+          if (i & 1) acc_p[h2] = Ops::mma(A, vop[s], acc_p[h2]);
+          else acc_s[h2] = Ops::mma(A, kop[s], acc_s[h2]);
+          return;
+        }
+        const int k = i - 2 * NPH;
+        const int h2 = k / NPH, jp = (k % NPH) / (2 * DTL), dt = (k % (2 * DTL)) >> 1;
+        if (k & 1) dk[dt] = Ops::mma(A, dsop[h2][jp], dk[dt]);
+        else dv[dt] = Ops::mma(A, pop[h2][jp], dv[dt]);
+      };
+      // P and dS of element r of half h2 (query row h2*32 + 8j + 4hh + i).
+      auto softmax_elem = [&](int h2, int r) __attribute__((always_inline)) {
+        const int j = r >> 2, i = r & 3;
+        const int row = h2 * 32 + j * 8 + hh * 4;
+        float x = fmaf(acc_s[h2][r], a.scale_log2, -l4[h2][j][i]);
+        if constexpr (decltype(mask_c)::value) {
+          if (kj > qt * kBwTile + row + i + a.q_offset) x = -INFINITY;
+        }
+        const float p = lc_exp2(x);
+        pop[h2][r >> 3][r & 7] = static_cast<T>(p);
+        dsop[h2][r >> 3][r & 7] = static_cast<T>(p * (acc_p[h2][r] - d4[h2][j][i]));
+      };
+      v8 ring[kBkRing];
+      read_rows(0);
+#pragma unroll
+      for (int i = 0; i < kBkRing; ++i) ring[i] = operand(i);
+#pragma unroll
+      for (int i = 0; i < 4 * NPH; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        const v8 A = ring[i % kBkRing];
+        mfma(i, A);
+        if (i + kBkRing < 4 * NPH) ring[i % kBkRing] = operand(i + kBkRing);
+        if (i == NPH) read_rows(1);
+        const int ph = i / NPH, e0 = (i % NPH) * EPS;
+        if (ph == 1 || ph == 2) {
+#pragma unroll
+          for (int e = 0; e < EPS; ++e) softmax_elem(ph - 1, e0 + e);
         }
       }
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-      for (int jp = 0; jp < 2; ++jp)
-#pragma unroll
-        for (int dt = 0; dt < DTL; ++dt) {
-          const int rowoff = (h2 * 32 + jp * 16) * ROW_B;
-          const i16x4_t olo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (LC_LDS i16x4_t*)(ol + ad.tr[0][dt] + rowoff));
-          const i16x4_t ohi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (LC_LDS i16x4_t*)(ol + ad.tr[1][dt] + rowoff));
-          dv[dt] = Ops::mma(__builtin_bit_cast(v8, __builtin_shufflevector(olo, ohi, 0, 1, 2, 3, 4, 5, 6, 7)),
-                            pop[h2][jp], dv[dt]);
-          const i16x4_t qlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (LC_LDS i16x4_t*)(ql + ad.tr[0][dt] + rowoff));
-          const i16x4_t qhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (LC_LDS i16x4_t*)(ql + ad.tr[1][dt] + rowoff));
-          dk[dt] = Ops::mma(__builtin_bit_cast(v8, __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7)),
-                            dsop[h2][jp], dk[dt]);
-        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
 
-  auto iteration = [&](int it, auto par_c) __attribute__((always_inline)) {
+  // MASK: false / true for tiles known to be unmasked / on the diagonal,
+  // kRuntimeMask to pick per tile (the bias path).
+  auto iteration = [&](int it, auto par_c, auto mask_c) __attribute__((always_inline)) {
     constexpr auto other = std::integral_constant<int, decltype(par_c)::value ^ 1>{};
-    if (key0 < a.Skv) load_bias(it);
-    if (it + 1 < n_iter) fetch(it + 1, other);
     const int qt = n_qt - 1 - it / a.G;
-    if (key0 < a.Skv) {
-      if (qt >= qt_nomask)
-        tile(qt, par_c, std::false_type{});
-      else
-        tile(qt, par_c, std::true_type{});
+    if constexpr (decltype(mask_c)::value == kRuntimeMask) {
+      if (key0 < a.Skv) load_bias(it);
+      if (it + 1 < n_iter) fetch(it + 1, other);
+      if (key0 < a.Skv) {
+        if (qt >= qt_nomask)
+          tile(qt, par_c, std::false_type{});
+        else
+          tile(qt, par_c, std::true_type{});
+      }
+    } else {
+      if (it + 1 < n_iter) fetch(it + 1, other);
+      tile(qt, par_c, mask_c);
     }
     pf_barrier<true>();
+  };
+  // Iterations [begin, end) with buffer parity it & 1.
+  auto run = [&](int begin, int end, auto mask_c) __attribute__((always_inline)) {
+    int it = begin;
+    if (it < end && (it & 1)) {
+      iteration(it, std::integral_constant<int, 1>{}, mask_c);
+      ++it;
+    }
+    for (; it + 1 < end; it += 2) {
+      iteration(it, std::integral_constant<int, 0>{}, mask_c);
+      iteration(it + 1, std::integral_constant<int, 1>{}, mask_c);
+    }
+    if (it < end) iteration(it, std::integral_constant<int, 0>{}, mask_c);
   };
 
   if (n_iter > 0) fetch(0, std::integral_constant<int, 0>{});
   pf_barrier<true>();
-  int it = 0;
-  for (; it + 1 < n_iter; it += 2) {
-    iteration(it, std::integral_constant<int, 0>{});
-    iteration(it + 1, std::integral_constant<int, 1>{});
+  if constexpr (BIAS != 0) {
+    run(0, n_iter, std::integral_constant<int, kRuntimeMask>{});
+  } else {
+    // Waves whose keys all lie past Skv run the tiles on zero K/V operands and
+    // store nothing; every wave passes the same barriers.
+    const int n_nomask = min(n_iter, max(0, n_qt - qt_nomask) * a.G);
+    run(0, n_nomask, std::false_type{});
+    run(n_nomask, n_iter, std::true_type{});
   }
-  if (it < n_iter) iteration(it, std::integral_constant<int, 0>{});
 
   if (!key_ok) return;
   store_transposed<T, DTL>(static_cast<T*>(a.dk) + b * a.dks[0] + (int64_t)kvh * a.dks[1] +
