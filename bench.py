@@ -422,9 +422,9 @@ def run_model(args):
         layer.value_pages.normal_(generator=gd)
     ids = torch.randint(0, cfg.vocab_size, (B, 1), generator=gd, device=dev)
     if args.tune_gemms:
-        # The projections stay torch matmuls; PyTorch's TunableOp picks the
-        # fastest hipBLASLt / rocBLAS solution per shape during the first eager
-        # step. A 1 GB rotating buffer keeps the weights out of the 256 MB
+        # The q/k/v and o projections stay torch matmuls (the MLP's run on
+        # lc_decode_linear); PyTorch's TunableOp picks the fastest hipBLASLt /
+        # rocBLAS solution per shape during the first eager step. A 1 GB rotating buffer keeps the weights out of the 256 MB
         # Infinity Cache while it times them, as in the real step. Tuning is
         # switched off again before the graph is captured.
         import tempfile
@@ -492,8 +492,9 @@ def run_model(args):
                    "batch": B, "context": ctx, "page_size": P, "layers": cfg.num_hidden_layers,
                    "hidden": cfg.hidden_size, "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size,
                    "hip_graph": True, "bytes_per_step": weights + kv,
-                   "projections": "torch matmul" + (", TunableOp-selected hipBLASLt/rocBLAS "
-                                                    "solutions" if args.tune_gemms else "")},
+                   "projections": "q/k/v and o: torch matmul" + (
+                       " (TunableOp-selected hipBLASLt/rocBLAS solutions)" if args.tune_gemms
+                       else "") + "; gate/up + SwiGLU and down: native lc_decode_linear"},
         "roofline": {"bound": "hbm", "kernel": "whole decode step (weights + KV read once)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),

@@ -176,6 +176,42 @@ LC_API int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, cons
                       float* max_logit, void* workspace, int64_t workspace_bytes, int dtype,
                       void* stream);
 
+/* Bytes of fp32 workspace lc_decode_linear needs for a given shape, mode and
+ * split request (split-K partials; 256 when the call runs unsplit), or -1 for
+ * invalid sizes. */
+LC_API int64_t lc_decode_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int mode,
+                                                int splits);
+
+/* Number of int32 ticket counters lc_decode_linear uses for N output columns
+ * (one per block of 128 columns, 64 in mode 1), or -1. */
+LC_API int64_t lc_decode_linear_counter_count(int64_t N, int mode);
+
+/* Projection of up to 32 rows (a decode step's batch), the weight streamed once:
+ *   mode 0: y[m, n] = round(x[m, :] . weight[n, :])                   n < N
+ *   mode 1: y[m, n] = round(silu(g) * u), g = round(x[m] . weight[n]),
+ *           u = round(x[m] . weight[N + n])                             n < N
+ * fp32 accumulation, round() to `dtype`, silu in fp32. Mode 0 replaces the
+ * nn.Linear projections of a decode step (models/llama3/attention.py:100-102
+ * q/k/v and :154 o_proj; mlp.py:35-37); mode 1 replaces
+ * swiglu(gate_proj(x), up_proj(x)) (mlp.py:39-43, kernels/triton/swiglu.py:15-42)
+ * over the concatenated [gate; up] weight [2N, K], with the reference's
+ * roundings (g and u rounded as the projections' outputs).
+ * x: [M, K] row stride x_row_stride; weight: [N or 2N, K] (nn.Linear layout);
+ * y: [M, N] row stride y_row_stride. bf16/f16; 1 <= M <= 32 (M == 0 is a
+ * no-op); K % 128 == 0; x and weight rows 16-byte aligned, y rows 8-byte
+ * aligned; weight and x each under 2 GiB.
+ * splits: K-splits (0 = enough workgroups to cover the CUs once). With more
+ * than one split the partial sums go through `workspace`
+ * (>= lc_decode_linear_workspace_bytes) and are added in split order by the
+ * last split to finish, so results do not depend on the split schedule.
+ * counters: lc_decode_linear_counter_count(N, mode) int32 values that are zero
+ * on entry; the call returns them to zero. Calls that overlap in time must not
+ * share workspace or counters. */
+LC_API int lc_decode_linear(const void* x, int64_t x_row_stride, const void* weight,
+                            int64_t weight_row_stride, void* y, int64_t y_row_stride, int64_t M,
+                            int64_t N, int64_t K, int mode, int splits, void* workspace,
+                            int64_t workspace_bytes, int* counters, int dtype, void* stream);
+
 /* Bytes of fp32 workspace lc_paged_decode_fwd needs for these sizes
  * (partial outputs and logsumexps of every split). */
 LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits);

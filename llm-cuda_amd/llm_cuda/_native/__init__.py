@@ -72,6 +72,13 @@ _SIGNATURES = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, ctypes.c_int,
          _c_p],
     ),
+    "lc_decode_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int]),
+    "lc_decode_linear_counter_count": (_c_i64, [_c_i64, ctypes.c_int]),
+    "lc_decode_linear": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int,
+         ctypes.c_int, _c_p, _c_i64, _c_p, ctypes.c_int, _c_p],
+    ),
     "lc_paged_decode_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "lc_paged_decode_fwd": (
         ctypes.c_int,

@@ -450,6 +450,90 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
 
 
 # ---------------------------------------------------------------------------
+# Decode-step projections  (reference: the nn.Linear calls of
+# models/llama3/attention.py:100-102,154 and mlp.py:35-43 at a decode step)
+# ---------------------------------------------------------------------------
+DECODE_LINEAR_MAX_ROWS = 32
+_DL_COUNTERS: dict = {}
+
+
+def _decode_linear_counters(dev: torch.device, n: int) -> torch.Tensor:
+    """Zeroed int32 ticket counters for lc_decode_linear (each call returns its
+    counters to zero, so one buffer per device serves every call on a stream)."""
+    key = (dev.type, dev.index)
+    buf = _DL_COUNTERS.get(key)
+    if buf is None or buf.numel() < n:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("decode_linear: run one call outside graph capture first "
+                               "(its ticket counters are allocated and zeroed eagerly)")
+        buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
+        _DL_COUNTERS[key] = buf
+    return buf
+
+
+def decode_linear_applies(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False) -> bool:
+    """True where decode_linear takes the call: bf16/f16 on the GPU, 1-32 rows,
+    K % 128 == 0, aligned rows, no autograd graph being recorded."""
+    if not (x.is_cuda and weight.is_cuda and x.dtype == weight.dtype
+            and x.dtype in (torch.bfloat16, torch.float16) and weight.dim() == 2):
+        return False
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    if not (1 <= rows <= DECODE_LINEAR_MAX_ROWS and K % 128 == 0 and weight.shape[1] == K):
+        return False
+    if swiglu and weight.shape[0] % 2:
+        return False
+    if _records_grad(x, weight):
+        return False
+    return (weight.stride(1) == 1 and weight.stride(0) % 8 == 0
+            and weight.data_ptr() % 16 == 0)
+
+
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False,
+                  splits: int = 0) -> torch.Tensor:
+    """Projection of a decode step's rows, the weight streamed once.
+
+    swiglu=False: x @ weight.T (weight [N, K], nn.Linear layout), rounded to
+    x's dtype. swiglu=True: weight is [gate; up] ([2N, K]) and the result is
+    swiglu(x @ gate.T, x @ up.T) with both projections rounded first (the
+    reference's gate_proj / up_proj outputs). x: [..., K] with at most 32 rows.
+    splits: K-splits (0 = the library's choice).
+    """
+    if _records_grad(x, weight):
+        raise RuntimeError("decode_linear is inference-only (autograd is recording)")
+    if x.dtype != weight.dtype:
+        raise TypeError("x and weight must share a dtype")
+    if weight.dim() != 2 or x.shape[-1] != weight.shape[1]:
+        raise ValueError(f"x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match")
+    dev = nat.require_device(x, weight)
+    K = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    weight = weight if weight.stride(-1) == 1 else weight.contiguous()
+    M = x2.shape[0]
+    N = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    y = torch.empty(*lead, N, dtype=x.dtype, device=dev)
+    if M == 0:
+        return y
+    mode = 1 if swiglu else 0
+    lib = nat.load()
+    ws_bytes = lib.lc_decode_linear_workspace_bytes(M, N, K, mode, int(splits))
+    if ws_bytes < 0:
+        raise ValueError(f"decode_linear: unsupported sizes M={M} N={N} K={K}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    counters = _decode_linear_counters(dev, lib.lc_decode_linear_counter_count(N, mode))
+    with _DeviceGuard(dev):
+        rc = lib.lc_decode_linear(
+            x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), y.data_ptr(), N,
+            M, N, K, mode, int(splits), ws.data_ptr(), ws.numel(), counters.data_ptr(),
+            nat.lc_dtype(x), _stream(dev))
+    nat.check(rc, "lc_decode_linear")
+    return y
+
+
+# ---------------------------------------------------------------------------
 # Paged decode  (reference: kernels/triton/decode_attention.py:204-287 over
 # models/llama3/kv_cache.py:65-83)
 # ---------------------------------------------------------------------------

@@ -3,11 +3,15 @@
 The projections are torch matmuls (hipBLASLt); the SwiGLU between them is the
 HIP kernel. For inference, gate and up come out of one GEMM against the
 concatenated weight and SwiGLU reads the two halves of its output in place.
+At a decode step (at most 32 rows, bf16/f16) gate, up and the SwiGLU are one
+native launch instead (`decode_linear(swiglu=True)`): the [gate; up] weight is
+streamed once and only the SwiGLU output is written, with the same roundings.
 """
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from llm_cuda.kernels import _ops
 from llm_cuda.kernels.triton.swiglu import triton_swiglu
 
 from .config import Llama3Config
@@ -27,6 +31,13 @@ class Llama3MLP(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if FusedLinearWeights.usable(self.gate_proj, self.up_proj):
             n = self.gate_proj.weight.shape[0]
-            gu = F.linear(x, self._gate_up.weight())
+            w = self._gate_up.weight()
+            if _ops.decode_linear_applies(x, w, swiglu=True):
+                h = _ops.decode_linear(x, w, swiglu=True)
+                wd = self.down_proj.weight
+                if _ops.decode_linear_applies(h, wd):
+                    return _ops.decode_linear(h, wd)
+                return self.down_proj(h)
+            gu = F.linear(x, w)
             return self.down_proj(triton_swiglu(gu[..., :n], gu[..., n:]))
         return self.down_proj(triton_swiglu(self.gate_proj(x), self.up_proj(x)))

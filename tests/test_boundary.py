@@ -49,6 +49,26 @@ def test_exports_nothing_else():
     assert exported == _declared()
 
 
+def test_decode_linear_arguments_rejected_before_launch():
+    from llm_cuda import _native
+
+    lib = _native.load()
+    assert lib.lc_decode_linear_counter_count(4096, 0) == 32
+    assert lib.lc_decode_linear_counter_count(14336, 1) == 224
+    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 2, 0) == -1
+    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 0, 1) == 256  # unsplit
+    # one fp32 partial of 128 x 32 values per (row block, split)
+    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 0, 8) == 32 * 8 * 4096 * 4
+    for M, K, mode, what in ((33, 512, 0, b"M=33"), (4, 500, 0, b"multiple of 128"),
+                             (4, 512, 3, b"mode 3")):
+        rc = lib.lc_decode_linear(16, K, 16, K, 16, 256, M, 256, K, mode, 0, 16, 1 << 20, 16, 2,
+                                  None)
+        assert rc == -1 and what in lib.lc_last_error(), lib.lc_last_error()
+    rc = lib.lc_decode_linear(16, 512, 16, 512, 16, 256, 4, 256, 512, 0, 0, 16, 1 << 20, 16, 0,
+                              None)
+    assert rc == -1 and b"dtype" in lib.lc_last_error()
+
+
 def test_invalid_arguments_rejected_before_launch():
     from llm_cuda import _native
 
