@@ -8,7 +8,9 @@ sequences, inputs resident in HBM. `value` = algorithmic bytes / step time.
 
 Other workloads (--workload): decode70b (config 5), prefill (config 3,
 TFLOP/s), prefill_bwd (the attention backward at the config-3 shape), lm_head
-(fused lm_head + greedy argmax at the config-4 vocab), model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
+(fused lm_head + greedy argmax at the config-4 vocab), decode_linear (the
+decode-step MLP projections on lc_decode_linear at the config-4 shape),
+model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
 swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
 (counter calibration copy).
 
@@ -379,6 +381,86 @@ def run_lm_head(args):
     return result
 
 
+def run_decode_linear(args):
+    """Decode-step MLP projections at the config-4 shape (32 rows): gate/up +
+    SwiGLU ([2 x 14336, 4096] weight, lc_decode_linear mode 1) followed by down
+    ([4096, 14336], mode 0), the reference's mlp.py:39-43 at a decode step."""
+    import torch
+    import torch.nn.functional as F
+
+    from llm_cuda.kernels import _ops
+
+    dev = torch.device("cuda", 0)
+    M, H, FF = 32, 4096, 14336
+    g = torch.Generator(device=dev).manual_seed(0)
+    # Four weight sets (1.4 GB) in rotation, so no step finds its weights in
+    # the 256 MB Infinity Cache (in the model each layer's weights are cold).
+    sets = [((torch.randn(2 * FF, H, generator=g, device=dev) * H ** -0.5).bfloat16(),
+             (torch.randn(H, FF, generator=g, device=dev) * FF ** -0.5).bfloat16())
+            for _ in range(4)]
+    x = torch.randn(M, H, generator=g, device=dev).bfloat16()
+    state = {"i": 0}
+
+    def step():
+        state["i"] = (state["i"] + 1) % len(sets)
+        wgu, wd = sets[state["i"]]
+        return _ops.decode_linear(_ops.decode_linear(x, wgu, swiglu=True), wd)
+
+    ms, wall = time_steps(step, args.steps, args.warmup)
+    nbytes = 3 * FF * H * 2 + M * (H + FF + H) * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    def torch_step():
+        state["i"] = (state["i"] + 1) % len(sets)
+        wgu, wd = sets[state["i"]]
+        gu = F.linear(x, wgu)
+        return F.linear(_ops.swiglu(gu[:, :FF], gu[:, FF:]), wd)
+
+    ms_t, _ = time_steps(torch_step, args.steps, args.warmup)
+    log(f"decode_linear: {ms * 1e3:.1f} us/step (gate/up + SwiGLU + down), {gbs:.0f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM); torch linear + SwiGLU kernel + linear "
+        f"(default solutions): {ms_t * 1e3:.1f} us")
+    result = {
+        "metric": "decode MLP projections GB/s",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 5),
+        "dtype": "bf16",
+        "config": {"workload": "decode-step MLP (gate/up + SwiGLU, down), Llama-3-8B shapes at "
+                               "batch 32 (BASELINE config 4 layer)", "rows": M, "hidden": H,
+                   "ffn": FF, "bytes_per_step": nbytes, "torch_ms": round(ms_t, 5)},
+        "roofline": {"bound": "hbm", "kernel": "decode_linear_kernel (2 launches)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("decode_linear_mlp_8b")},
+    }
+    if not args.no_cpu_baseline:
+        from oracle.elementwise import swiglu
+        from oracle.lm_head import lm_head_logits
+
+        torch.set_num_threads(cpu_threads())
+        xs = x.cpu()
+        wgu, wd = (w.cpu() for w in sets[0])
+        # 1/8 of the output columns of each projection (a bounded sample)
+        cols = FF // 8
+        wg_s, wu_s, wd_s = wgu[:cols], wgu[FF:FF + cols], wd[:H // 8]
+
+        def cpu_step():
+            h = swiglu(lm_head_logits(xs, wg_s), lm_head_logits(xs, wu_s)).bfloat16()
+            hfull = torch.zeros(M, FF, dtype=torch.bfloat16)
+            hfull[:, :cols] = h
+            return lm_head_logits(hfull, wd_s)
+
+        secs = timed_cpu(cpu_step, budget_s=30.0)
+        sbytes = nbytes / 8
+        result["cpu_baseline"] = {
+            "value": round(sbytes / secs / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1/8 of each projection's output columns (fp64 dot products, "
+                      f"oracle.lm_head.lm_head_logits + oracle.elementwise.swiglu): {secs:.3f} s"}
+    return result
+
+
 def _model8b_config():
     from llm_cuda.models.llama3.config import Llama3Config
 
@@ -697,7 +779,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--workload", default="decode8b",
                         choices=["decode8b", "decode70b", "prefill", "prefill_bwd", "model8b",
-                                 "lm_head", "copycal",
+                                 "lm_head", "decode_linear", "copycal",
                                  "rmsnorm", "swiglu", "rope"])
     parser.add_argument("--split-tokens", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -737,6 +819,8 @@ def main() -> int:
         res = run_prefill_bwd(args)
     elif args.workload == "lm_head":
         res = run_lm_head(args)
+    elif args.workload == "decode_linear":
+        res = run_decode_linear(args)
     elif args.workload == "copycal":
         res = run_copycal(args)
     elif args.workload in ("rmsnorm", "swiglu", "rope"):
