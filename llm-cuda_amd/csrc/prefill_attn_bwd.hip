@@ -1,7 +1,8 @@
 // Causal attention backward (dQ, dK, dV) with native GQA, no atomics.
 //
 // Given the forward's output O and natural-log logsumexp L, and dO:
-//   delta_i = sum_d dO_id O_id                      (attn_bwd_delta_kernel)
+//   delta_i = sum_d dO_id O_id                      (in the MFMA dQ kernel, or
+//                                                    attn_bwd_delta_kernel)
 //   P_ij    = exp(s_ij - L_i),  s_ij = q_i.k_j * scale + bias_ij
 //             (keys j <= i + q_offset; bias: the optional additive mask)
 //   dS_ij   = P_ij (dO_i.v_j - delta_i)
@@ -38,6 +39,10 @@ struct BwdArgs {
   const float* lse;    // [B, Hq, Sq], natural log
   const float* delta;  // [B, Hq, Sq]
   const float* lse2;   // [B, Hq, Sq], lse * log2(e), +inf where lse = -inf
+  // The forward's output: the MFMA dQ kernel forms delta and lse2 itself and
+  // writes them for the dK/dV kernel (the generic path runs the delta kernel).
+  const void* o;
+  int64_t os[4];
   void* dq;
   void* dk;
   void* dv;
@@ -466,8 +471,29 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
   load_row_operand<T, DPAD>(qop, static_cast<const T*>(a.q) + b * a.qs[0] + (int64_t)head * a.qs[1] + (int64_t)qi * a.qs[2], row_ok, hh, a.D);
   load_row_operand<T, DPAD>(doop, static_cast<const T*>(a.dout) + b * a.dos[0] + (int64_t)head * a.dos[1] + (int64_t)qi * a.dos[2], row_ok, hh, a.D);
   const int64_t ridx = ((int64_t)b * a.Hq + head) * a.Sq + qi;
-  const float lse2 = row_ok ? a.lse2[ridx] : INFINITY;
-  const float dl = row_ok ? a.delta[ridx] : 0.f;
+  // delta = rowsum(dO * O) of this lane's row: the O row in dO's operand
+  // layout (lane half hh holds dims hh*DPAD/2 ..), fp32 products in dim
+  // order within each half, then the two halves added; lse2 = lse * log2(e)
+  // (+inf for a row that saw no key, so its probabilities are exactly 0).
+  // Both go to the workspace for the dK/dV kernel.
+  float dl, lse2;
+  {
+    v8 oop[KS];
+    load_row_operand<T, DPAD>(oop, static_cast<const T*>(a.o) + b * a.os[0] + (int64_t)head * a.os[1] + (int64_t)qi * a.os[2], row_ok, hh, a.D);
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        part = fmaf(static_cast<float>(oop[s][e]), static_cast<float>(doop[s][e]), part);
+    dl = part + __shfl_xor(part, 32, 64);
+    const float l = row_ok ? a.lse[ridx] : -INFINITY;
+    lse2 = l == -INFINITY ? INFINITY : l * kLog2e;
+    if (row_ok && hh == 0) {
+      const_cast<float*>(a.delta)[ridx] = dl;
+      const_cast<float*>(a.lse2)[ridx] = lse2;
+    }
+  }
 
   // Additive bias of the tile, loaded before its products (see BiasTile).
   constexpr int besz = BIAS == 2 ? 4 : 2;
@@ -1057,13 +1083,17 @@ int launch_delta(const void* o, const int64_t* o_strides, const BwdArgs& a, floa
 template <typename T>
 int run_bwd(const void* o, const int64_t* o_strides, BwdArgs a, float* delta, float* lse2,
             bool mfma, hipStream_t st) {
-  int rc = launch_delta<T>(o, o_strides, a, delta, lse2, st);
-  if (rc != LC_OK) return rc;
   a.delta = delta;
   a.lse2 = lse2;
+  a.o = o;
+  for (int i = 0; i < 4; ++i) a.os[i] = o_strides[i];
   if constexpr (!std::is_same<T, float>::value) {
+    // The dQ kernel forms delta and lse2 for every query row (an empty query
+    // side needs neither).
     if (mfma) return launch_bwd_mfma<T>(a, st);
   }
+  int rc = launch_delta<T>(o, o_strides, a, delta, lse2, st);
+  if (rc != LC_OK) return rc;
   return launch_bwd_generic<T>(a, st);
 }
 
@@ -1155,11 +1185,11 @@ int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, const void*
   float* lse2 = delta + need / 8;
   const int64_t esz = lc_dtype_size(dtype);
   bool mfma = (dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16) && D % 8 == 0 && D <= 128;
-  for (const void* p : {q, k, v, dout, (const void*)dq, (const void*)dk, (const void*)dv}) mfma = mfma && lc_aligned(p, 16);
+  for (const void* p : {q, k, v, o, dout, (const void*)dq, (const void*)dk, (const void*)dv}) mfma = mfma && lc_aligned(p, 16);
   for (int i = 0; i < 3; ++i)
     mfma = mfma && q_strides[i] % 8 == 0 && k_strides[i] % 8 == 0 && v_strides[i] % 8 == 0 &&
-           do_strides[i] % 8 == 0 && dq_strides[i] % 8 == 0 && dk_strides[i] % 8 == 0 &&
-           dv_strides[i] % 8 == 0;
+           o_strides[i] % 8 == 0 && do_strides[i] % 8 == 0 && dq_strides[i] % 8 == 0 &&
+           dk_strides[i] % 8 == 0 && dv_strides[i] % 8 == 0;
   // Buffer descriptors cover one head's rows with 32-bit byte offsets.
   mfma = mfma && (Skv * k_strides[2] + D) * esz < (1LL << 31) &&
          (Skv * v_strides[2] + D) * esz < (1LL << 31) &&

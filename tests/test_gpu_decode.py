@@ -102,6 +102,20 @@ def test_paged_ragged_random_permutation(cuda, dtype, P):
     assert_lse_close(lse, ref_lse)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("P", [16, 48])
+@pytest.mark.parametrize("D", [64, 48])
+def test_paged_lanes_kernel_small_head_dim(cuda, dtype, P, D):
+    """Page sizes that are not multiples of 32 take the per-lane-page kernel;
+    head_dim <= 64 runs its 64-wide instance (a tighter register budget)."""
+    lens = [1, 17, 64, 100, 333, 48]
+    q, kp, vp, bt, sl = _paged_case(lens, 8, 2, D, P, dtype, cuda, seed=P + D)
+    out, lse = _run_paged(q, kp, vp, bt, sl, cuda)
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert_close(out, ref, ATOL[dtype], f"lanes P={P} D={D}")
+    assert_lse_close(lse, ref_lse)
+
+
 def test_paged_empty_sequence_and_invalid_entries(cuda):
     lens = [0, 70, 130]
     q, kp, vp, bt, sl = _paged_case(lens, 4, 1, 64, 64, torch.bfloat16, cuda, seed=3)
