@@ -330,6 +330,12 @@ int launch_swiglu(const void* g, const void* u, void* o, int64_t rows, int64_t c
 // built as cat(freqs, freqs) are honoured (models/llama3/rotary.py:81-109
 // semantics, not the half-table shortcut of kernels/triton/rope.py:106-108).
 // ---------------------------------------------------------------------------
+// 16-byte chunks per lane of the vectorised RoPE kernel. At the bandwidth
+// shape (Q [4,32,4096,128] + K [4,8,4096,128] views) one chunk per lane ran at
+// 57.7 us, two at 60.8 us and four at 66.7 us: the activation stream is half
+// writes, and more bytes in flight per lane do not raise it.
+constexpr int kRopeItems = 1;
+
 struct RopeTensor {
   const void* x;
   void* out;
@@ -342,77 +348,94 @@ struct RopeTensor {
 // reciprocal sequence; 64-bit division is a long expansion that measurably
 // slows this HBM-bound kernel, so it is used only for grids of 2^32 lanes or
 // more.
-template <typename T, int VEC, typename I>
+// ITEMS: chunks per lane, grid-strided (item it of lane g is chunk
+// g + it * lanes). Every item's loads are issued, from clamped indices and
+// with no branch between them, before the first item is computed, so a lane
+// keeps ITEMS x 32 bytes of activations in flight.
+template <typename T, int VEC, typename I, int ITEMS>
 __global__ __launch_bounds__(256) void rope_kernel(RopeTensor t1, RopeTensor t2,
                                                    const T* __restrict__ cos,
                                                    const T* __restrict__ sin, int64_t cs_s,
                                                    int64_t sn_s, int S, int half,
                                                    int64_t rows1, int64_t rows_total) {
   const I chunks = static_cast<I>(half / VEC);
-  const I gid = static_cast<I>(blockIdx.x) * static_cast<I>(blockDim.x) + threadIdx.x;
-  const I row = gid / chunks;
-  if (row >= static_cast<I>(rows_total)) return;
-  const int d0 = static_cast<int>(gid - row * chunks) * VEC;
+  const I lanes = static_cast<I>(gridDim.x) * static_cast<I>(blockDim.x);
+  const I gid0 = static_cast<I>(blockIdx.x) * static_cast<I>(blockDim.x) + threadIdx.x;
+  const I total = static_cast<I>(rows_total) * chunks;
 
-  const bool second = row >= static_cast<I>(rows1);
-  const RopeTensor& t = second ? t2 : t1;
-  const I r = second ? row - static_cast<I>(rows1) : row;
-  // Rows are ordered (b, s, h), heads fastest: neighbouring rows share one
-  // cos/sin row (served from L1 after the first), and for activations laid
-  // out as [B, S, H, D] projection views they are also adjacent in memory.
-  const I nh = static_cast<I>(t.h);
-  const I bs = r / nh;
-  const int64_t h = static_cast<int64_t>(r - bs * nh);
-  const I bi = bs / static_cast<I>(S);
-  const int s = static_cast<int>(bs - bi * static_cast<I>(S));
-  const int64_t b = static_cast<int64_t>(bi);
+  struct Item {
+    const T* xp;
+    T* op;
+    const T* cp;
+    const T* sp;
+    int d0;
+  };
+  // Addresses of chunk g (rows ordered (b, s, h), heads fastest: neighbouring
+  // rows share one cos/sin row, served from L1 after the first, and for
+  // activations laid out as [B, S, H, D] projection views they are also
+  // adjacent in memory).
+  auto locate = [&](I g) -> Item {
+    const I row = g / chunks;
+    const int d0 = static_cast<int>(g - row * chunks) * VEC;
+    const bool second = row >= static_cast<I>(rows1);
+    const RopeTensor& t = second ? t2 : t1;
+    const I r = second ? row - static_cast<I>(rows1) : row;
+    const I nh = static_cast<I>(t.h);
+    const I bs = r / nh;
+    const int64_t h = static_cast<int64_t>(r - bs * nh);
+    const I bi = bs / static_cast<I>(S);
+    const int s = static_cast<int>(bs - bi * static_cast<I>(S));
+    const int64_t b = static_cast<int64_t>(bi);
+    Item it;
+    it.xp = static_cast<const T*>(t.x) + b * t.xs[0] + h * t.xs[1] + (int64_t)s * t.xs[2];
+    it.op = static_cast<T*>(t.out) + b * t.os[0] + h * t.os[1] + (int64_t)s * t.os[2];
+    it.cp = cos + (int64_t)s * cs_s;
+    it.sp = sin + (int64_t)s * sn_s;
+    it.d0 = d0;
+    return it;
+  };
 
-  const T* xp = static_cast<const T*>(t.x) + b * t.xs[0] + h * t.xs[1] + (int64_t)s * t.xs[2];
-  T* op = static_cast<T*>(t.out) + b * t.os[0] + h * t.os[1] + (int64_t)s * t.os[2];
-  const T* cp = cos + (int64_t)s * cs_s;
-  const T* sp = sin + (int64_t)s * sn_s;
-
-  float x1[VEC], x2[VEC], c1[VEC], c2[VEC], s1[VEC], s2[VEC];
   if constexpr (VEC * sizeof(T) == 16) {
-    Vec16<T> a = EW_LD(xp + d0), bb = EW_LD(xp + d0 + half);
-    Vec16<T> ca = lc_load16(cp + d0), cb = lc_load16(cp + d0 + half);
-    Vec16<T> sa = lc_load16(sp + d0), sb = lc_load16(sp + d0 + half);
+    if (gid0 >= total) return;
+    Item itm[ITEMS];
+    Vec16<T> xa[ITEMS], xb[ITEMS], ca[ITEMS], cb[ITEMS], sa[ITEMS], sb[ITEMS];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      x1[e] = lc_to_f32(a.v[e]);
-      x2[e] = lc_to_f32(bb.v[e]);
-      c1[e] = lc_to_f32(ca.v[e]);
-      c2[e] = lc_to_f32(cb.v[e]);
-      s1[e] = lc_to_f32(sa.v[e]);
-      s2[e] = lc_to_f32(sb.v[e]);
+    for (int k = 0; k < ITEMS; ++k) {
+      const I g = min(gid0 + static_cast<I>(k) * lanes, total - 1);
+      itm[k] = locate(g);
+      xa[k] = EW_LD(itm[k].xp + itm[k].d0);
+      xb[k] = EW_LD(itm[k].xp + itm[k].d0 + half);
+      ca[k] = lc_load16(itm[k].cp + itm[k].d0);
+      cb[k] = lc_load16(itm[k].cp + itm[k].d0 + half);
+      sa[k] = lc_load16(itm[k].sp + itm[k].d0);
+      sb[k] = lc_load16(itm[k].sp + itm[k].d0 + half);
+    }
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      Vec16<T> o1, o2;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float x1 = lc_to_f32(xa[k].v[e]), x2 = lc_to_f32(xb[k].v[e]);
+        o1.v[e] = lc_from_f32<T>(lc_rope_lo(x1, x2, lc_to_f32(ca[k].v[e]), lc_to_f32(sa[k].v[e])));
+        o2.v[e] = lc_from_f32<T>(lc_rope_hi(x1, x2, lc_to_f32(cb[k].v[e]), lc_to_f32(sb[k].v[e])));
+      }
+      if (gid0 + static_cast<I>(k) * lanes < total) {
+        EW_ST(itm[k].op + itm[k].d0, o1);
+        EW_ST(itm[k].op + itm[k].d0 + half, o2);
+      }
     }
   } else {
+    if (gid0 >= total) return;
+    const Item it = locate(gid0);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      x1[e] = lc_to_f32(xp[d0 + e]);
-      x2[e] = lc_to_f32(xp[d0 + e + half]);
-      c1[e] = lc_to_f32(cp[d0 + e]);
-      c2[e] = lc_to_f32(cp[d0 + e + half]);
-      s1[e] = lc_to_f32(sp[d0 + e]);
-      s2[e] = lc_to_f32(sp[d0 + e + half]);
+      const float x1 = lc_to_f32(it.xp[it.d0 + e]);
+      const float x2 = lc_to_f32(it.xp[it.d0 + e + half]);
+      it.op[it.d0 + e] = lc_from_f32<T>(
+          lc_rope_lo(x1, x2, lc_to_f32(it.cp[it.d0 + e]), lc_to_f32(it.sp[it.d0 + e])));
+      it.op[it.d0 + e + half] = lc_from_f32<T>(lc_rope_hi(
+          x1, x2, lc_to_f32(it.cp[it.d0 + e + half]), lc_to_f32(it.sp[it.d0 + e + half])));
     }
-  }
-  Vec16<T> o1, o2;
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    const T lo = lc_from_f32<T>(lc_rope_lo(x1[e], x2[e], c1[e], s1[e]));
-    const T hi = lc_from_f32<T>(lc_rope_hi(x1[e], x2[e], c2[e], s2[e]));
-    if constexpr (VEC * sizeof(T) == 16) {
-      o1.v[e] = lo;
-      o2.v[e] = hi;
-    } else {
-      op[d0 + e] = lo;
-      op[d0 + e + half] = hi;
-    }
-  }
-  if constexpr (VEC * sizeof(T) == 16) {
-    EW_ST(op + d0, o1);
-    EW_ST(op + d0 + half, o2);
   }
 }
 
@@ -433,26 +456,28 @@ int launch_rope(const RopeTensor& t1, const RopeTensor& t2, const void* cos, con
   const int64_t rows1 = B * t1.h * S;
   const int64_t rows_total = rows1 + B * t2.h * S;
   const int vec = vec_ok ? V : 1;
-  const int64_t threads_total = rows_total * (half / vec);
+  const int64_t chunks_total = rows_total * (half / vec);
   const int threads = 256;
-  const int64_t blocks = lc_cdiv(threads_total, threads);
+  const int items = vec_ok ? kRopeItems : 1;
+  const int64_t blocks = lc_cdiv(lc_cdiv(chunks_total, items), threads);
   LC_REQUIRE(blocks < (1LL << 31), "lc_rope_fwd: problem too large");
   if (blocks == 0) return LC_OK;
-  const bool idx32 = blocks * threads < (1LL << 32);
-#define LC_ROPE(VEC_, I_)                                                                 \
-  rope_kernel<T, VEC_, I_><<<(unsigned)blocks, threads, 0, st>>>(                         \
+  // 32-bit indices while every chunk index (and a clamped item's) fits
+  const bool idx32 = chunks_total + (int64_t)blocks * threads * items < (1LL << 32);
+#define LC_ROPE(VEC_, I_, IT_)                                                            \
+  rope_kernel<T, VEC_, I_, IT_><<<(unsigned)blocks, threads, 0, st>>>(                    \
       t1, t2, static_cast<const T*>(cos), static_cast<const T*>(sin), cs_s, sn_s, (int)S, \
       (int)half, rows1, rows_total)
   if (vec_ok) {
     if (idx32)
-      LC_ROPE(V, uint32_t);
+      LC_ROPE(V, uint32_t, kRopeItems);
     else
-      LC_ROPE(V, int64_t);
+      LC_ROPE(V, int64_t, kRopeItems);
   } else {
     if (idx32)
-      LC_ROPE(1, uint32_t);
+      LC_ROPE(1, uint32_t, 1);
     else
-      LC_ROPE(1, int64_t);
+      LC_ROPE(1, int64_t, 1);
   }
 #undef LC_ROPE
   return lc_check_launch("lc_rope_fwd");
