@@ -506,14 +506,18 @@ def run_model(args):
     if args.tune_gemms:
         # The q/k/v and o projections stay torch matmuls (the MLP's run on
         # lc_decode_linear); PyTorch's TunableOp picks the fastest hipBLASLt /
-        # rocBLAS solution per shape during the first eager step. A 1 GB rotating buffer keeps the weights out of the 256 MB
-        # Infinity Cache while it times them, as in the real step. Tuning is
-        # switched off again before the graph is captured.
+        # rocBLAS solution per shape during the first eager step. A 1 GB
+        # rotating buffer keeps the weights out of the 256 MB Infinity Cache
+        # while it times them, as in the real step. Tuning is switched off
+        # again before the graph is captured.
         import tempfile
 
         tun = torch.cuda.tunable
         tun.set_filename(os.path.join(tempfile.gettempdir(), f"lcuda_tunableop_{os.getpid()}.csv"))
         tun.set_rotating_buffer_size(1024)
+        if args.gemm_tuning_ms:
+            tun.set_max_tuning_duration(args.gemm_tuning_ms)
+            tun.set_max_tuning_iterations(100000)
         tun.enable(True)
         tun.tuning_enable(True)
 
@@ -533,6 +537,11 @@ def run_model(args):
         eager_logits = eager_logits.float().clone()
         if args.tune_gemms:
             torch.cuda.tunable.tuning_enable(False)
+            try:
+                for r in torch.cuda.tunable.get_results():
+                    log("TunableOp pick: " + " | ".join(str(f) for f in r)[:220])
+            except Exception as exc:  # diagnostics only
+                log(f"TunableOp results unavailable: {exc}")
         # warm the allocator on a side stream, then capture
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -785,6 +794,9 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gemm-tuning", dest="tune_gemms", action="store_false",
                         help="model8b: keep torch's default GEMM solutions (no TunableOp)")
+    parser.add_argument("--gemm-tuning-ms", type=int, default=0,
+                        help="model8b: TunableOp's time budget per candidate solution (ms; "
+                             "0 = torch's default)")
     parser.add_argument("--prefill-shape", default=None, metavar="B,Hq,Hkv,S,D",
                         help="prefill: another shape instead of config 3 (4,32,8,4096,128)")
     parser.add_argument("--no-secondary", dest="secondary", action="store_false",
