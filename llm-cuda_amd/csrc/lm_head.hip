@@ -9,13 +9,15 @@
 //
 // Kernels:
 //   * lm_head_argmax_mfma_kernel (bf16/f16, K % 128 == 0, up to 32 hidden rows
-//     per launch): a workgroup owns 128 vocab rows and streams their weight rows
-//     through LDS in 128-column tiles (buffer-to-LDS DMA, 256-byte runs per row,
-//     a three-stage ring with two tiles in flight), together with the matching
-//     128 columns of the hidden rows. Each wave computes
+//     per launch): a workgroup owns 64 vocab rows and streams their weight rows
+//     through LDS in 256-column tiles (buffer-to-LDS DMA, 512-byte runs per
+//     row, a three-stage ring with two tiles in flight), together with the
+//     matching 256 columns of the hidden rows. Its 4 waves are 2 row groups x
+//     2 column halves; each computes
 //     logits^T[32 vocab x 32 batch] += W[32 x 16] hidden^T[16 x 32] on
-//     v_mfma_f32_32x32x16; the epilogue rounds, takes each batch row's best
-//     (value, index) over the workgroup's 128 rows and writes it as a partial.
+//     v_mfma_f32_32x32x16 over its half, the halves are added through LDS, and
+//     the epilogue rounds, takes each batch row's best (value, index) over the
+//     workgroup's 64 rows and writes it as a partial.
 //   * lm_head_argmax_generic_kernel (any dtype / K): one lane per vocab row.
 //   * lm_head_argmax_reduce_kernel: one workgroup per batch row reduces the
 //     partials to the final id (int64) and, optionally, the winning logit.
@@ -33,9 +35,15 @@ namespace {
 
 using namespace lc_attn;
 
+// A workgroup: 2 row groups of 32 vocab rows x 2 halves of each tile's
+// columns, one wave each. 512-byte runs per row: at one workgroup per CU a
+// stream of 64 rows x 512 B tiles measured 5.85 TB/s against 5.49 TB/s for
+// 128 rows x 256 B (same bytes per tile).
 constexpr int kLhWaves = 4;
-constexpr int kLhRows = 32 * kLhWaves;  // vocab rows per workgroup
-constexpr int kLhKc = 128;              // hidden columns per tile (256-byte runs per row)
+constexpr int kLhRowWaves = 2;
+constexpr int kLhRows = 32 * kLhRowWaves;  // vocab rows per workgroup
+constexpr int kLhKc = 256;              // hidden columns per tile (512-byte runs per row)
+constexpr int kLhKHalf = kLhKc / 2;     // columns of a tile per wave
 constexpr int kLhStages = 3;            // LDS ring depth: two tiles in flight
 // (deeper rings, and 64-column tiles, measured no faster)
 // Cache policy of the weight loads: non-temporal. Each weight byte is read
@@ -62,6 +70,12 @@ __device__ __forceinline__ void lh_take(float& bv, int& bi, float xv, int xi) {
   }
 }
 
+// LDS swizzle of the 512-byte tile rows: 16-byte chunk c of row r sits at
+// c ^ s(r), s a permutation of 0..15 over 16 consecutive rows (the 256-byte
+// rows' swizzle), so the 16 lanes of an operand read (16 rows, one chunk) hit
+// 16 different 16-byte bank groups.
+__device__ __forceinline__ int lh_swz(int r) { return pf_swz<16>(r); }
+
 // s_waitcnt immediate: vmcnt(vm) lgkmcnt(lgkm), expcnt not waited on.
 constexpr int lh_waitcnt(int vm, int lgkm) {
   return (vm & 0xF) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
@@ -81,7 +95,7 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
   constexpr int ROW_B = kLhKc * (int)sizeof(T);  // bytes per row per tile
-  constexpr int KS = kLhKc / 16;                  // MFMA k-steps per tile
+  constexpr int KS = kLhKHalf / 16;               // MFMA k-steps per wave per tile
   constexpr int CPR = ROW_B / 16;
   constexpr int RPI = 64 / CPR;                   // rows per 1 KB DMA instruction
   constexpr int NIW_W = kLhRows / (RPI * kLhWaves);
@@ -94,8 +108,8 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   __shared__ __align__(16) char h0[H_B];
   __shared__ __align__(16) char h1[H_B];
   __shared__ __align__(16) char h2[H_B];
-  __shared__ float red_v[kLhWaves][32];
-  __shared__ int red_i[kLhWaves][32];
+  __shared__ float red_v[kLhRowWaves][32];
+  __shared__ int red_i[kLhRowWaves][32];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -103,6 +117,8 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int l32 = lane & 31;
   const int hh = lane >> 5;
+  const int rw = wave_s % kLhRowWaves;  // row group
+  const int kh = wave_s / kLhRowWaves;  // column half of each tile
   const int v0 = blockIdx.x * kLhRows;
   const int rows_valid = min(kLhRows, a.V - v0);
   const T* wbase = static_cast<const T*>(a.weight) + (int64_t)v0 * a.ws;
@@ -115,7 +131,7 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
 #pragma unroll
     for (int u = 0; u < NIW_W; ++u) {
       const int row = (wave * NIW_W + u) * RPI + lane / CPR;
-      const int ch = (lane % CPR) ^ pf_swz<CPR>(row);
+      const int ch = (lane % CPR) ^ lh_swz(row);
       o.o[u] = static_cast<int>(((int64_t)row * a.ws + ch * 8) * sizeof(T));
     }
     return o;
@@ -125,7 +141,7 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
 #pragma unroll
     for (int u = 0; u < NIW_H; ++u) {
       const int row = (wave * NIW_H + u) * RPI + lane / CPR;
-      const int ch = (lane % CPR) ^ pf_swz<CPR>(row);
+      const int ch = (lane % CPR) ^ lh_swz(row);
       // Rows past B get an offset of 2^31 bytes: beyond the descriptor's
       // range (< 2^31) with any tile offset added, so they load zeros, and
       // their row * stride is never formed (it may not fit 32 bits).
@@ -135,11 +151,12 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
     return o;
   }();
   // Operand reads: row l32 (of the wave's 32 vocab rows, or of the hidden
-  // rows), k = hh * 64 + 8 s .. + 8 in the tile.
+  // rows), 16-byte chunk kh*16 + hh*8 + s of the tile row at k-step s.
   int raddr[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) raddr[s] = l32 * ROW_B + (((hh * (CPR / 2) + s) ^ pf_swz<CPR>(l32)) << 4);
-  const int wrow0 = wave * 32 * ROW_B;
+  for (int s = 0; s < KS; ++s)
+    raddr[s] = l32 * ROW_B + (((kh * (CPR / 2) + hh * (CPR / 4) + s) ^ lh_swz(l32)) << 4);
+  const int wrow0 = rw * 32 * ROW_B;
 
   auto wbuf = [&](auto st_c) __attribute__((always_inline)) -> LC_LDS char* {
     constexpr int S = decltype(st_c)::value;
@@ -176,7 +193,10 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   // flight), barrier (every wave's part of tile t landed, every wave done with
   // tile t-1), refill tile t-1's stage with tile t+2, compute tile t.
   static_assert(kLhStages == 3, "the loop below is written for a three-stage ring");
-  const int n_tiles = a.K / kLhKc;
+  // K a multiple of 128: with an odd number of half tiles the last tile's
+  // second half is past K, and its waves skip that tile's products.
+  const int n_tiles = (a.K + kLhKc - 1) / kLhKc;
+  const bool skip_last = kh == 1 && (a.K % kLhKc) != 0;
   constexpr int kNi = NIW_W + NIW_H;  // DMA instructions per wave per tile
   auto iteration = [&](int t, auto st_c) __attribute__((always_inline)) {
     constexpr int S = decltype(st_c)::value;
@@ -188,7 +208,7 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
     __builtin_amdgcn_s_barrier();
     lc_compiler_fence();
     if (t + 2 < n_tiles) fetch(t + 2, std::integral_constant<int, (S + 2) % 3>{});
-    compute(st_c);
+    if (!(skip_last && t + 1 == n_tiles)) compute(st_c);
   };
 
   using I0 = std::integral_constant<int, 0>;
@@ -202,25 +222,38 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
     if (t + 2 < n_tiles) iteration(t + 2, I2{});
   }
 
-  // Epilogue: lane (l32, hh) holds batch row l32 and vocab rows
-  // v0 + wave*32 + 8j + 4hh + i for register 4j + i.
+  // The second column half hands its sums to the first through LDS (the W
+  // ring is free after the barrier), added in a fixed order.
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[0][r] += acc[1][r];
+  __syncthreads();
+  float* half = reinterpret_cast<float*>(w0);
+  if (kh == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) half[(rw * 16 + r) * 64 + lane] = acc[0][r];
+  }
+  __syncthreads();
+  // Epilogue (first-half waves): lane (l32, hh) holds batch row l32 and vocab
+  // rows v0 + rw*32 + 8j + 4hh + i for register 4j + i.
   float bv = -INFINITY;
   int bi = INT_MAX;
+  if (kh == 0) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = wave * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-    const float x = lc_to_f32(lc_from_f32<T>(acc[0][r] + acc[1][r]));
-    if (row < rows_valid) lh_take(bv, bi, x, v0 + row);
-  }
-  lh_take(bv, bi, __shfl_xor(bv, 32, 64), __shfl_xor(bi, 32, 64));
-  if (hh == 0) {
-    red_v[wave][l32] = bv;
-    red_i[wave][l32] = bi;
+    for (int r = 0; r < 16; ++r) {
+      const int row = rw * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+      const float x = lc_to_f32(lc_from_f32<T>(acc[0][r] + half[(rw * 16 + r) * 64 + lane]));
+      if (row < rows_valid) lh_take(bv, bi, x, v0 + row);
+    }
+    lh_take(bv, bi, __shfl_xor(bv, 32, 64), __shfl_xor(bi, 32, 64));
+    if (hh == 0) {
+      red_v[rw][l32] = bv;
+      red_i[rw][l32] = bi;
+    }
   }
   __syncthreads();
   if (wave == 0 && hh == 0) {
 #pragma unroll
-    for (int w = 1; w < kLhWaves; ++w) lh_take(bv, bi, red_v[w][l32], red_i[w][l32]);
+    for (int w = 1; w < kLhRowWaves; ++w) lh_take(bv, bi, red_v[w][l32], red_i[w][l32]);
     if (l32 < a.B) {
       a.part_val[(int64_t)blockIdx.x * a.pstride + l32] = bv;
       a.part_idx[(int64_t)blockIdx.x * a.pstride + l32] = bi;
@@ -369,7 +402,7 @@ int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void*
   a.K = (int)K;
   a.V = (int)V;
   const int64_t esz = lc_dtype_size(dtype);
-  const bool mfma = (dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16) && K % kLhKc == 0 &&
+  const bool mfma = (dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16) && K % kLhKHalf == 0 &&
                     lc_aligned(hidden, 16) && lc_aligned(weight, 16) &&
                     hidden_row_stride % 8 == 0 && weight_row_stride % 8 == 0 &&
                     ((int64_t)kLhRows * weight_row_stride) * esz < (1LL << 31) &&
