@@ -177,13 +177,13 @@ LC_API int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, cons
                       void* stream);
 
 /* Bytes of fp32 workspace lc_decode_linear needs for a given shape, mode and
- * split request (split-K partials; 256 when the call runs unsplit), or -1 for
- * invalid sizes. */
+ * split request (two partials per workgroup; 256 when every workgroup's share
+ * is whole row blocks), or -1 for invalid sizes. */
 LC_API int64_t lc_decode_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int mode,
                                                 int splits);
 
-/* Number of int32 ticket counters lc_decode_linear uses for N output columns
- * (one per block of 128 columns, 64 in mode 1), or -1. */
+/* Number of int32 ticket counters lc_decode_linear needs for N output columns
+ * (one per block of 64 columns, 32 in mode 1), or -1. */
 LC_API int64_t lc_decode_linear_counter_count(int64_t N, int mode);
 
 /* Projection of up to 32 rows (a decode step's batch), the weight streamed once:
@@ -200,10 +200,12 @@ LC_API int64_t lc_decode_linear_counter_count(int64_t N, int mode);
  * y: [M, N] row stride y_row_stride. bf16/f16; 1 <= M <= 32 (M == 0 is a
  * no-op); K % 128 == 0; x and weight rows 16-byte aligned, y rows 8-byte
  * aligned; weight and x each under 2 GiB.
- * splits: K-splits (0 = enough workgroups to cover the CUs once). With more
- * than one split the partial sums go through `workspace`
- * (>= lc_decode_linear_workspace_bytes) and are added in split order by the
- * last split to finish, so results do not depend on the split schedule.
+ * The weight's (row block, K tile) units are dealt to the workgroups in equal
+ * contiguous shares. splits: workgroups per row block (0 = as few workgroups
+ * as give each no more units than an even spread over the CUs). A row block
+ * shared by several workgroups is summed through `workspace`
+ * (>= lc_decode_linear_workspace_bytes) in workgroup order by the last of
+ * them to finish, so results do not depend on the schedule.
  * counters: lc_decode_linear_counter_count(N, mode) int32 values that are zero
  * on entry; the call returns them to zero. Calls that overlap in time must not
  * share workspace or counters. */

@@ -90,6 +90,49 @@ __device__ __forceinline__ void pf_dma_tile(const void* base, int nbytes, LC_LDS
   }
 }
 
+// pf_dma_tile issued as inline assembly, for streaming rings that keep more
+// than one tile in flight: the same rows, offsets and zero fill; NT selects
+// non-temporal loads (data read once). The compiler does not see these LDS
+// writes. Issued through the builtin, it tracks them and, unable to tell a
+// ring's stages apart, waits for every DMA in flight (the next tiles'
+// included) before each LDS read, which leaves one tile in flight. The
+// kernel's own s_waitcnt vmcnt + barrier must order its LDS reads after the
+// data; the "memory" clobber keeps the compiler from moving LDS accesses
+// across the DMA.
+template <int NIW, int RPI, int ROW_B, bool NT>
+__device__ __forceinline__ void pf_dma_tile_untracked(const void* base, int nbytes,
+                                                      LC_LDS char* dst, int wave,
+                                                      const PfLoadOffsets<NIW>& off, int soff) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const u32x4_t rsrc = {
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b))),
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(b >> 32))) & 0xFFFFu,
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(nbytes)), 0x00020000u};
+  const int so = __builtin_amdgcn_readfirstlane(soff);
+#pragma unroll
+  for (int u = 0; u < NIW; ++u) {
+    const int row0 = (wave * NIW + u) * RPI;
+    const int m0v = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(reinterpret_cast<uintptr_t>(dst + row0 * ROW_B)));
+    // M0 (the LDS destination) is saved and restored around the load.
+    int m0_saved;
+    if constexpr (NT)
+      __asm__ __volatile__(
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+          "buffer_load_dwordx4 %1, %2, %4 offen nt lds\n\ts_mov_b32 m0, %0"
+          : "=&s"(m0_saved)
+          : "v"(off.o[u]), "s"(rsrc), "s"(m0v), "s"(so)
+          : "memory");
+    else
+      __asm__ __volatile__(
+          "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+          "buffer_load_dwordx4 %1, %2, %4 offen lds\n\ts_mov_b32 m0, %0"
+          : "=&s"(m0_saved)
+          : "v"(off.o[u]), "s"(rsrc), "s"(m0v), "s"(so)
+          : "memory");
+  }
+}
+
 // Additive bias of one 64-key tile for the query row of each lane, in the
 // layout of the 32x32 S^T accumulators: lane (l32 = query row, hh = lane / 32)
 // holds keys k0 + kt*32 + j*8 + hh*4 + e (kt < 2, j < 4, e < 4), i.e. register

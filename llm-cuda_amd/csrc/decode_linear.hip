@@ -11,20 +11,31 @@
 // with the same roundings: g and u are rounded as the two projections'
 // outputs before the SwiGLU, which is computed in fp32.
 //
-// Kernel: a workgroup of 4 waves owns 128 weight rows (mode 1: 64 gate rows
-// and the 64 matching up rows) and streams them through LDS in 128-column
-// tiles (buffer-to-LDS DMA, 256-byte runs per row, non-temporal, a
-// three-stage ring with two tiles in flight), with the matching columns of the
-// x rows. Each wave computes y^T[32 weight rows x 32 x rows] on
-// v_mfma_f32_32x32x16. HBM-bound: the weight is read once; x (<= 256 KiB at
-// K 4096) is re-read from L2 by every workgroup.
+// Work: the weight is cut into row blocks of ROWS rows (mode 1: ROWS/2 gate
+// rows and the ROWS/2 matching up rows) and each block into K tiles of
+// 16384 / ROWS columns (32 KiB of weight per tile). The (block, tile) units,
+// block-major, are dealt out in equal contiguous runs to the workgroups of a
+// one-dimensional grid (stream-K): every workgroup streams the same number of
+// tiles, whatever the block count, so a grid of one workgroup per CU finishes
+// together.
 //
-// Split-K: with few row blocks (N = 4096 gives 32) the K tiles are divided
-// over grid.y splits so that the grid fills the CUs. Each split writes its
-// fp32 partial to the workspace; a per-row-block ticket picks the last split
-// to arrive, which sums the partials in split order (the result does not
-// depend on which split came last), runs the epilogue and returns the ticket
-// counter to zero. No second launch.
+// Kernel: 4 waves. ROWS = 128: wave w owns block rows 32w .. 32w + 31 over a
+// 128-column tile (256-byte runs per row). ROWS = 64 (K % 256 == 0): wave w
+// owns rows 32 (w % 2) .. + 31 over columns 128 (w / 2) .. + 127 of a
+// 256-column tile (512-byte runs per row), and the two column halves are
+// added through LDS when a block's run ends. Tiles stream through LDS
+// (buffer-to-LDS DMA, non-temporal weight loads, a three-stage ring with two
+// tiles in flight, kept running across block boundaries) with the matching
+// columns of the x rows; each wave computes y^T[32 weight rows x 32 x rows]
+// on v_mfma_f32_32x32x16. HBM-bound: the weight is read once; x (<= 1 MiB) is
+// re-read from L2 by every workgroup.
+//
+// A block whose units are split over several workgroups: each writes its fp32
+// partial to the workspace, slot (workgroup, 0) for the first block of its run
+// and (workgroup, 1) for the last. A per-block ticket picks the last to
+// arrive, which sums the partials in workgroup order (the result does not
+// depend on which came last), runs the epilogue and returns the ticket counter
+// to zero. No second launch, and no workgroup waits for another.
 #include <limits.h>
 #include <algorithm>
 #include <math.h>
@@ -41,15 +52,13 @@ using namespace lc_attn;
 // (Two-wave workgroups for mode 1 -- 448 row blocks of 32 columns, two per
 // CU, instead of 224 blocks on 256 CUs -- measured slower.)
 constexpr int kDlWaves = 4;
-constexpr int kDlRows = 32 * kDlWaves;  // weight rows per workgroup
-constexpr int kDlKc = 128;              // K columns per tile (256-byte runs per row)
 constexpr int kDlBatch = 32;            // x rows per launch (the MFMA's N)
-constexpr int kDlPartFloats = kDlRows * kDlBatch;  // fp32 partial of one split (16 per thread)
+constexpr int kDlTileElems = 16384;     // weight elements per tile: ROWS x columns
+constexpr int kDlKc = 128;              // K granularity: columns per wave per tile
 // Output columns per row block.
-constexpr int dl_out_cols(int mode) { return mode == 1 ? kDlRows / 2 : kDlRows; }
-constexpr int kDlWeightAux = 2;         // non-temporal weight loads (read once)
-constexpr int kDlMaxBlocks = 1 << 16;   // row blocks per launch (ticket counters)
-constexpr int kDlMaxSplits = 16;        // K-splits per launch
+constexpr int dl_out_cols(int mode, int rows) { return mode == 1 ? rows / 2 : rows; }
+constexpr int kDlMaxBlocks = 1 << 17;   // row blocks per launch (ticket counters)
+constexpr int kDlSumBatch = 8;          // partials loaded per batch by the summing workgroup
 constexpr int kDlCoherent = 16;         // buffer cache policy sc1: agent-coherent access
 
 __device__ __forceinline__ float dl_silu_mul(float g, float u) {
@@ -67,32 +76,45 @@ struct DlArgs {
   const void* x;
   const void* w;
   void* y;
-  float* part;    // [n_blocks][splits][kDlPartFloats]
+  float* part;    // [grid][2][ROWS * 32] partials of a workgroup's first / last block
   int* counters;  // [n_blocks], zero between calls
   int64_t xs, ws, ys;  // row strides (elements)
   int M, K, N;         // N = output columns
-  int tiles_per_split, splits;
+  int kt;              // K tiles per row block
+  int n_blocks;
 };
 
-template <typename T, int MODE>
+// First unit of workgroup g's run when U units are dealt to G workgroups.
+__device__ __forceinline__ int dl_run_begin(int64_t g, int64_t U, int64_t G) {
+  return static_cast<int>(g * U / G);
+}
+// The workgroup whose run holds unit u.
+__device__ __forceinline__ int dl_owner(int64_t u, int64_t U, int64_t G) {
+  return static_cast<int>(((u + 1) * G - 1) / U);
+}
+
+template <typename T, int MODE, int ROWS>
 __global__ __launch_bounds__(64 * kDlWaves) void decode_linear_kernel(DlArgs a) {
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
-  constexpr int ROW_B = kDlKc * (int)sizeof(T);
-  constexpr int KS = kDlKc / 16;
+  constexpr int KC = kDlTileElems / ROWS;       // columns per tile
+  constexpr int ROW_B = KC * (int)sizeof(T);    // bytes per row per tile
+  constexpr int RW = ROWS / 32;                 // waves along the rows
+  constexpr int KP = kDlWaves / RW;             // waves along K (kDlKc columns each)
+  constexpr int KS = kDlKc / 16;                // MFMA k-steps per wave per tile
   constexpr int CPR = ROW_B / 16;
   constexpr int RPI = 64 / CPR;
-  constexpr int NIW_W = kDlRows / (RPI * kDlWaves);
+  constexpr int NIW_W = ROWS / (RPI * kDlWaves);
   constexpr int NIW_H = kDlBatch / (RPI * kDlWaves);
-  constexpr int W_B = kDlRows * ROW_B;
+  constexpr int W_B = ROWS * ROW_B;
   constexpr int H_B = kDlBatch * ROW_B;
-  constexpr int OUT_COLS = dl_out_cols(MODE);  // output columns per block
-  __shared__ __align__(16) char w0[W_B];
-  __shared__ __align__(16) char w1[W_B];
-  __shared__ __align__(16) char w2[W_B];
-  __shared__ __align__(16) char h0[H_B];
-  __shared__ __align__(16) char h1[H_B];
-  __shared__ __align__(16) char h2[H_B];
+  constexpr int STAGE_B = W_B + H_B;
+  constexpr int OUTC = dl_out_cols(MODE, ROWS);  // output columns per block
+  constexpr int PF = ROWS * kDlBatch;            // floats of one partial (16 per holding thread)
+  constexpr int XK_B = KP > 1 ? (kDlWaves - RW) * 16 * 64 * 4 : 0;  // column-half exchange
+  constexpr int XU_B = MODE == 1 ? (RW / 2) * 16 * 64 * 4 : 0;       // up-value exchange
+  static_assert(KP * RW == kDlWaves && KC == KP * kDlKc && KP <= 2, "tile geometry");
+  __shared__ __align__(16) char lds[3 * STAGE_B + XK_B + XU_B];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -101,30 +123,30 @@ __global__ __launch_bounds__(64 * kDlWaves) void decode_linear_kernel(DlArgs a) 
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-  const int blk = blockIdx.x;
-  const int split = blockIdx.y;
-  const int c0 = blk * OUT_COLS;  // first output column of the block
-  const int cols_valid = min(OUT_COLS, a.N - c0);
-  const int t_begin = split * a.tiles_per_split;
-  const int n_tiles = min(a.tiles_per_split, a.K / kDlKc - t_begin);
+  const int rw = wave % RW;  // row group: block rows 32 rw .. 32 rw + 31
+  const int kh = wave / RW;  // column part: tile columns kDlKc kh .. + kDlKc - 1
+  // Waves of column part 0 hold a block's sums once the parts are added.
+  const bool holder = kh == 0;
+  const int kt = a.kt;
+  const int64_t U = (int64_t)a.n_blocks * kt;
+  const int64_t G = gridDim.x;
+  const int g = blockIdx.x;
+  const int u_begin = dl_run_begin(g, U, G);
+  const int n = dl_run_begin(g + 1, U, G) - u_begin;
+  const int first_blk = u_begin / kt;
 
-  // Weight rows of the block: mode 0 rows c0 .. c0 + 127; mode 1 gate rows
-  // c0 .. c0 + 63 (block rows 0-63) and up rows N + c0 .. (block rows 64-127).
-  // Offsets are taken from row c0. Rows past the matrix are past the
+  // Per-lane DMA offsets from a block's first weight row: mode 0 rows
+  // 0 .. ROWS-1; mode 1 gate rows 0 .. ROWS/2-1 (block rows 0 .. ROWS/2-1)
+  // and up rows N .. N+ROWS/2-1. Rows past the matrix are past the
   // descriptor's range and land in LDS as zeros; gate rows past N read up
   // rows (their outputs are not stored).
-  const T* wbase = static_cast<const T*>(a.w) + (int64_t)c0 * a.ws + (int64_t)t_begin * kDlKc;
-  const int64_t last_row = MODE == 1 ? (int64_t)a.N + cols_valid - 1 : (int64_t)cols_valid - 1;
-  const int wbytes = static_cast<int>((last_row * a.ws + (int64_t)(a.K - t_begin * kDlKc)) * sizeof(T));
-  const T* xbase = static_cast<const T*>(a.x) + (int64_t)t_begin * kDlKc;
-  const int xbytes = static_cast<int>(((int64_t)(a.M - 1) * a.xs + (a.K - t_begin * kDlKc)) * sizeof(T));
   const PfLoadOffsets<NIW_W> woff = [&] {
     PfLoadOffsets<NIW_W> o;
 #pragma unroll
     for (int u = 0; u < NIW_W; ++u) {
       const int row = (wave * NIW_W + u) * RPI + lane / CPR;
-      const int ch = (lane % CPR) ^ pf_swz<CPR>(row);
-      const int64_t wrow = MODE == 1 && row >= kDlRows / 2 ? (int64_t)a.N + row - kDlRows / 2 : row;
+      const int ch = (lane % CPR) ^ pf_swz<16>(row);
+      const int64_t wrow = MODE == 1 && row >= ROWS / 2 ? (int64_t)a.N + row - ROWS / 2 : row;
       o.o[u] = static_cast<int>((wrow * a.ws + ch * 8) * sizeof(T));
     }
     return o;
@@ -134,194 +156,243 @@ __global__ __launch_bounds__(64 * kDlWaves) void decode_linear_kernel(DlArgs a) 
 #pragma unroll
     for (int u = 0; u < NIW_H; ++u) {
       const int row = (wave * NIW_H + u) * RPI + lane / CPR;
-      const int ch = (lane % CPR) ^ pf_swz<CPR>(row);
+      const int ch = (lane % CPR) ^ pf_swz<16>(row);
       // Rows past M: an offset past the descriptor's range (< 2^31) with any
       // tile offset added, so they load zeros.
       o.o[u] = row < a.M ? static_cast<int>(((int64_t)row * a.xs + ch * 8) * sizeof(T)) : INT_MIN;
     }
     return o;
   }();
+  const int xbytes = static_cast<int>(((int64_t)(a.M - 1) * a.xs + a.K) * sizeof(T));
+  // LDS chunk c of row r sits at position c ^ pf_swz<16>(r); lane (l32, hh)
+  // reads chunks kh*16 + hh*8 + s (k-step s) of row l32 -- the same k order
+  // for the weight rows and the x rows.
   int raddr[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) raddr[s] = l32 * ROW_B + (((hh * (CPR / 2) + s) ^ pf_swz<CPR>(l32)) << 4);
-  const int wrow0 = wave * 32 * ROW_B;
+  for (int s = 0; s < KS; ++s)
+    raddr[s] = l32 * ROW_B + (((kh * 16 + hh * 8 + s) ^ pf_swz<16>(l32)) << 4);
+  const int wrow0 = rw * 32 * ROW_B;
 
-  auto wbuf = [&](auto st_c) __attribute__((always_inline)) -> LC_LDS char* {
-    constexpr int S = decltype(st_c)::value;
-    if constexpr (S == 0) return (LC_LDS char*)w0;
-    else if constexpr (S == 1) return (LC_LDS char*)w1;
-    else return (LC_LDS char*)w2;
-  };
-  auto hbuf = [&](auto st_c) __attribute__((always_inline)) -> LC_LDS char* {
-    constexpr int S = decltype(st_c)::value;
-    if constexpr (S == 0) return (LC_LDS char*)h0;
-    else if constexpr (S == 1) return (LC_LDS char*)h1;
-    else return (LC_LDS char*)h2;
-  };
-  auto fetch = [&](int t, auto st_c) __attribute__((always_inline)) {
-    pf_dma_tile<NIW_W, RPI, ROW_B, kDlWeightAux>(wbase, wbytes, wbuf(st_c), wave_s, woff, t * ROW_B);
-    pf_dma_tile<NIW_H, RPI, ROW_B>(xbase, xbytes, hbuf(st_c), wave_s, hoff, t * ROW_B);
+  // DMA cursor: the block and tile of the next unit to fetch.
+  int f_blk = first_blk;
+  int f_t = u_begin - first_blk * kt;
+  auto fetch = [&](int stage) __attribute__((always_inline)) {
+    const int c0 = f_blk * OUTC;
+    const int cols_valid = min(OUTC, a.N - c0);
+    const int64_t last_row = MODE == 1 ? (int64_t)a.N + cols_valid - 1 : (int64_t)cols_valid - 1;
+    const T* wbase = static_cast<const T*>(a.w) + (int64_t)c0 * a.ws;
+    const int wbytes = static_cast<int>((last_row * a.ws + a.K) * sizeof(T));
+    LC_LDS char* dst = (LC_LDS char*)lds + stage * STAGE_B;
+    pf_dma_tile_untracked<NIW_W, RPI, ROW_B, true>(wbase, wbytes, dst, wave_s, woff, f_t * ROW_B);
+    pf_dma_tile_untracked<NIW_H, RPI, ROW_B, false>(a.x, xbytes, dst + W_B, wave_s, hoff, f_t * ROW_B);
+    if (++f_t == kt) {
+      f_t = 0;
+      ++f_blk;
+    }
   };
 
   f32x16_t acc[2];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-  auto compute = [&](auto st_c) __attribute__((always_inline)) {
-    LC_LDS const char* wl = wbuf(st_c) + wrow0;
-    LC_LDS const char* hl = hbuf(st_c);
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  };
+  zero_acc();
+  auto compute = [&](int stage) __attribute__((always_inline)) {
+    LC_LDS const char* wl = (LC_LDS const char*)lds + stage * STAGE_B + wrow0;
+    LC_LDS const char* hl = (LC_LDS const char*)lds + stage * STAGE_B + W_B;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       acc[s & 1] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(wl + raddr[s]),
                             *reinterpret_cast<LC_LDS const v8*>(hl + raddr[s]), acc[s & 1]);
   };
 
-  // Iteration t: wait for tile t (this wave's DMA; tile t+1 may still be in
-  // flight), barrier (every wave's part of tile t landed, every wave done with
-  // tile t-1), refill tile t-1's stage with tile t+2, compute tile t.
+  // End of a block's run in this workgroup: add the column parts, combine
+  // with the block's other workgroups if it is split, and (in the workgroup
+  // that completes it) store the block's outputs. Every wave takes the same
+  // path through the barriers (s_last is read by all after a barrier).
+  auto finish_block = [&](int blk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[0][r] += acc[1][r];
+    if constexpr (KP > 1) {
+      // (The exchange area is not touched again before every wave has passed
+      // the next tile's barrier.)
+      float* xk = reinterpret_cast<float*>(lds + 3 * STAGE_B);
+      if (!holder) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xk[(((kh - 1) * RW + rw) * 16 + r) * 64 + lane] = acc[0][r];
+      }
+      __syncthreads();
+      if (holder) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][r] += xk[(rw * 16 + r) * 64 + lane];
+      }
+    }
+    const int blk_lo = blk * kt;
+    const int run_lo = u_begin;
+    const int run_hi = u_begin + n;
+    if (run_lo > blk_lo || run_hi < blk_lo + kt) {
+      // Partial of this run: register r of holding thread tid at
+      // [slot][tid][16] (four 16-byte runs), so the summing workgroup's
+      // thread tid gets the same (row, x row) back. The partials travel
+      // through stores and loads with the sc1 cache policy (agent-coherent:
+      // performed past the per-XCD L2s, as agent-scope atomics are), so no
+      // cache-wide write-back or invalidate is needed: each lane waits for
+      // its stores to be acknowledged before the workgroup takes its ticket.
+      const int slot = g * 2 + (blk == first_blk ? 0 : 1);
+      if (holder) {
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            a.part + (int64_t)slot * PF, 0, PF * 4, 0x00020000);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4_t v = {acc[0][4 * q], acc[0][4 * q + 1], acc[0][4 * q + 2], acc[0][4 * q + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs, tid * 64 + 16 * q,
+                                                 0, kDlCoherent);
+        }
+      }
+      const int g_first = dl_owner(blk_lo, U, G);
+      const int g_last = dl_owner(blk_lo + kt - 1, U, G);
+      __builtin_amdgcn_s_waitcnt(dl_waitcnt(0, 0));
+      __syncthreads();
+      if (tid == 0) {
+        const int ticket = __hip_atomic_fetch_add(a.counters + blk, 1, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        s_last = ticket == g_last - g_first;
+      }
+      __syncthreads();
+      if (!s_last) return;
+      if (holder) {
+        // The block's partials in workgroup order: the first workgroup's is
+        // its last-block slot unless its run starts at this block.
+        const int first_slot =
+            g_first * 2 + (dl_run_begin(g_first, U, G) < blk_lo ? 1 : 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][r] = 0.f;
+        for (int gb = g_first; gb <= g_last; gb += kDlSumBatch) {
+          u32x4_t pv[kDlSumBatch][4];
+#pragma unroll
+          for (int i = 0; i < kDlSumBatch; ++i)
+            if (gb + i <= g_last) {
+              const int sl = gb + i == g_first ? first_slot : (gb + i) * 2;
+              const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                  a.part + (int64_t)sl * PF, 0, PF * 4, 0x00020000);
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                pv[i][q] = __builtin_amdgcn_raw_buffer_load_b128(prs, tid * 64 + 16 * q, 0,
+                                                                 kDlCoherent);
+            }
+#pragma unroll
+          for (int i = 0; i < kDlSumBatch; ++i)
+            if (gb + i <= g_last) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const f32x4_t v = __builtin_bit_cast(f32x4_t, pv[i][q]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[0][4 * q + e] += v[e];
+              }
+            }
+        }
+      }
+      if (tid == 0)
+        __hip_atomic_store(a.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // Epilogue. Holding lane (l32, hh) of row group rw holds x row l32 and
+    // block rows rw*32 + 8j + 4hh + i (register 4j + i).
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const int c0 = blk * OUTC;
+    const int cols_valid = min(OUTC, a.N - c0);
+    T* yrow = static_cast<T*>(a.y) + (int64_t)l32 * a.ys + c0;
+    if constexpr (MODE == 0) {
+      if (!holder || l32 >= a.M) return;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = rw * 32 + j * 8 + hh * 4;
+        t4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = lc_from_f32<T>(acc[0][j * 4 + i]);
+        if (col + 4 <= cols_valid) {
+          *reinterpret_cast<t4*>(yrow + col) = o;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (col + i < cols_valid) yrow[col + i] = o[i];
+        }
+      }
+    } else {
+      // The upper row groups hold the up rows of the columns the lower ones
+      // hold the gate rows of; the rounded up values go through LDS.
+      constexpr int HALF = RW / 2;
+      float* ux = reinterpret_cast<float*>(lds + 3 * STAGE_B + XK_B);
+      if (holder && rw >= HALF) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          ux[((rw - HALF) * 16 + r) * 64 + lane] = lc_to_f32(lc_from_f32<T>(acc[0][r]));
+      }
+      __syncthreads();
+      if (!holder || rw >= HALF || l32 >= a.M) return;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = rw * 32 + j * 8 + hh * 4;
+        t4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = j * 4 + i;
+          const float gv = lc_to_f32(lc_from_f32<T>(acc[0][r]));
+          o[i] = lc_from_f32<T>(dl_silu_mul(gv, ux[(rw * 16 + r) * 64 + lane]));
+        }
+        if (col + 4 <= cols_valid) {
+          *reinterpret_cast<t4*>(yrow + col) = o;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (col + i < cols_valid) yrow[col + i] = o[i];
+        }
+      }
+    }
+  };
+
+  // Iteration i: wait for tile i (this wave's DMA; tile i+1 may still be in
+  // flight), barrier (every wave's part of tile i landed, every wave done with
+  // tile i-1 and with the exchange areas), refill tile i-1's stage with tile
+  // i+2, compute tile i; at the last tile of a block's run, finish the block.
   constexpr int kNi = NIW_W + NIW_H;  // DMA instructions per wave per tile
-  auto iteration = [&](int t, auto st_c) __attribute__((always_inline)) {
-    constexpr int S = decltype(st_c)::value;
-    if (t + 1 < n_tiles)
+  fetch(0);
+  if (n > 1) fetch(1);
+  int stage = 0;
+  int c_blk = first_blk;
+  int c_t = u_begin - first_blk * kt;
+  for (int i = 0; i < n; ++i) {
+    if (i + 1 < n)
       __builtin_amdgcn_s_waitcnt(dl_waitcnt(kNi, 0));
     else
       __builtin_amdgcn_s_waitcnt(dl_waitcnt(0, 0));
     lc_compiler_fence();
     __builtin_amdgcn_s_barrier();
     lc_compiler_fence();
-    if (t + 2 < n_tiles) fetch(t + 2, std::integral_constant<int, (S + 2) % 3>{});
-    compute(st_c);
-  };
-
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  fetch(0, I0{});
-  if (n_tiles > 1) fetch(1, I1{});
-  for (int t = 0; t < n_tiles; t += 3) {
-    iteration(t, I0{});
-    if (t + 1 < n_tiles) iteration(t + 1, I1{});
-    if (t + 2 < n_tiles) iteration(t + 2, I2{});
-  }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) acc[0][r] += acc[1][r];
-
-  if (a.splits > 1) {
-    // Partial of this split: register r of lane (wave, lane) at r*256 + tid,
-    // so the reading workgroup's thread tid gets the same (row, x row) back.
-    // The partials travel through stores and loads with the sc1 cache policy
-    // (agent-coherent: performed past the per-XCD L2s, as agent-scope
-    // atomics are), so no cache-wide write-back or invalidate is needed: each
-    // lane waits for its stores to be acknowledged before the workgroup takes
-    // its ticket. Thread tid's 16 values sit at [tid][16] (four 16-byte runs).
-    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        a.part + (int64_t)blk * a.splits * kDlPartFloats, 0, a.splits * kDlPartFloats * 4,
-        0x00020000);
-    const int my_off = (split * kDlPartFloats + tid * 16) * 4;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4_t v = {acc[0][4 * q], acc[0][4 * q + 1], acc[0][4 * q + 2], acc[0][4 * q + 3]};
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs, my_off + 16 * q, 0,
-                                             kDlCoherent);
+    if (i + 2 < n) fetch(stage == 0 ? 2 : stage - 1);
+    compute(stage);
+    stage = stage == 2 ? 0 : stage + 1;
+    if (c_t == kt - 1 || i == n - 1) {
+      finish_block(c_blk);
+      zero_acc();
     }
-    __builtin_amdgcn_s_waitcnt(dl_waitcnt(0, 0));
-    __syncthreads();
-    if (tid == 0) {
-      const int ticket = __hip_atomic_fetch_add(a.counters + blk, 1, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-      s_last = ticket == a.splits - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // Every split's loads are issued before the first is waited for (up to
-    // kDlMaxSplits splits), then summed in split order.
-    u32x4_t pv[kDlMaxSplits][4];
-#pragma unroll
-    for (int sp = 0; sp < kDlMaxSplits; ++sp)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (sp < a.splits)
-          pv[sp][q] = __builtin_amdgcn_raw_buffer_load_b128(
-              prs, (sp * kDlPartFloats + tid * 16) * 4 + 16 * q, 0, kDlCoherent);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[0][r] = 0.f;
-#pragma unroll
-    for (int sp = 0; sp < kDlMaxSplits; ++sp)
-      if (sp < a.splits) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4_t v = __builtin_bit_cast(f32x4_t, pv[sp][q]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[0][4 * q + e] += v[e];
-        }
-      }
-    if (tid == 0)
-      __hip_atomic_store(a.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  // Epilogue. Lane (l32, hh) of wave w holds x row l32 and block rows
-  // w*32 + 8j + 4hh + i (register 4j + i).
-  typedef T t4 __attribute__((ext_vector_type(4)));
-  T* yrow = static_cast<T*>(a.y) + (int64_t)l32 * a.ys;
-  if constexpr (MODE == 0) {
-    if (l32 >= a.M) return;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = wave * 32 + j * 8 + hh * 4;
-      t4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = lc_from_f32<T>(acc[0][j * 4 + i]);
-      if (col + 4 <= cols_valid) {
-        *reinterpret_cast<t4*>(yrow + c0 + col) = o;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (col + i < cols_valid) yrow[c0 + col + i] = o[i];
-      }
-    }
-  } else {
-    // The upper half of the waves holds the up rows of the columns the lower
-    // half holds the gate rows of; the rounded up values go through LDS (the
-    // W ring is free now).
-    __syncthreads();
-    float* ux = reinterpret_cast<float*>(w0);
-    constexpr int HALF = kDlWaves / 2;
-    if (wave >= HALF) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        ux[((wave - HALF) * 16 + r) * 64 + lane] = lc_to_f32(lc_from_f32<T>(acc[0][r]));
-    }
-    __syncthreads();
-    if (wave >= HALF || l32 >= a.M) return;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = wave * 32 + j * 8 + hh * 4;
-      t4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = j * 4 + i;
-        const float g = lc_to_f32(lc_from_f32<T>(acc[0][r]));
-        o[i] = lc_from_f32<T>(dl_silu_mul(g, ux[(wave * 16 + r) * 64 + lane]));
-      }
-      if (col + 4 <= cols_valid) {
-        *reinterpret_cast<t4*>(yrow + c0 + col) = o;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (col + i < cols_valid) yrow[c0 + col + i] = o[i];
-      }
+    if (++c_t == kt) {
+      c_t = 0;
+      ++c_blk;
     }
   }
 }
 
-// Split count: enough workgroups to cover the CUs once, at most one split per
-// K tile. A request > 0 is honoured (clamped to the tile count).
-int dl_splits(int n_blocks, int k_tiles, int requested, int n_cu) {
-  int s = requested > 0 ? requested : std::max(1, n_cu / std::max(1, n_blocks));
-  s = std::min(std::min(s, k_tiles), kDlMaxSplits);
-  const int tps = (k_tiles + s - 1) / s;
-  return (k_tiles + tps - 1) / tps;
+// Workgroups for U = n_blocks * k_tiles units: with a request, `requested`
+// per row block (at most one per unit); otherwise the fewest that give no
+// workgroup more units than an even spread over the CUs does.
+int64_t dl_grid(int64_t n_blocks, int64_t k_tiles, int requested, int n_cu) {
+  const int64_t U = n_blocks * k_tiles;
+  if (requested > 0) return std::min<int64_t>(U, n_blocks * requested);
+  const int64_t per = (U + n_cu - 1) / n_cu;
+  return (U + per - 1) / per;
 }
 
 int dl_n_cu() {
@@ -337,24 +408,44 @@ int dl_n_cu() {
   return cached;
 }
 
+// Rows per block: 64 (512-byte runs per row) where K allows 256-column
+// tiles, else 128.
+int dl_rows(int64_t K) { return K % (2 * kDlKc) == 0 ? 64 : 128; }
+
+struct DlPlan {
+  int rows;
+  int64_t n_blocks, k_tiles, grid, workspace;
+};
+
+bool dl_plan(int64_t N, int64_t K, int mode, int splits, DlPlan* p) {
+  if (N <= 0 || K <= 0 || K % kDlKc || (mode != 0 && mode != 1) || splits < 0) return false;
+  p->rows = dl_rows(K);
+  const int64_t out_cols = dl_out_cols(mode, p->rows);
+  p->n_blocks = (N + out_cols - 1) / out_cols;
+  if (p->n_blocks > kDlMaxBlocks) return false;
+  p->k_tiles = K / (kDlTileElems / p->rows);
+  p->grid = dl_grid(p->n_blocks, p->k_tiles, splits, dl_n_cu());
+  const int64_t U = p->n_blocks * p->k_tiles;
+  // No partials when every run is a whole number of whole blocks.
+  const bool whole = U % p->grid == 0 && (U / p->grid) % p->k_tiles == 0;
+  p->workspace = whole ? 256 : (p->grid * 2 * p->rows * kDlBatch * 4 + 255) / 256 * 256;
+  return true;
+}
+
 }  // namespace
 
 extern "C" {
 
 int64_t lc_decode_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int mode, int splits) {
-  if (M < 0 || N <= 0 || K <= 0 || (mode != 0 && mode != 1) || splits < 0) return -1;
-  const int64_t out_cols = dl_out_cols(mode);
-  const int64_t n_blocks = (N + out_cols - 1) / out_cols;
-  if (n_blocks > kDlMaxBlocks) return -1;
-  const int k_tiles = (int)std::max<int64_t>(1, K / kDlKc);
-  const int s = dl_splits((int)n_blocks, k_tiles, splits, dl_n_cu());
-  if (s <= 1) return 256;
-  return (n_blocks * s * kDlPartFloats * 4 + 255) / 256 * 256;
+  DlPlan p;
+  if (M < 0 || !dl_plan(N, K, mode, splits, &p)) return -1;
+  return p.workspace;
 }
 
 int64_t lc_decode_linear_counter_count(int64_t N, int mode) {
   if (N <= 0 || (mode != 0 && mode != 1)) return -1;
-  const int64_t out_cols = dl_out_cols(mode);
+  // Enough for the smaller row block (64 rows).
+  const int64_t out_cols = dl_out_cols(mode, 64);
   return (N + out_cols - 1) / out_cols;
 }
 
@@ -387,14 +478,13 @@ int lc_decode_linear(const void* x, int64_t x_row_stride, const void* weight,
   LC_REQUIRE(w_rows * weight_row_stride * esz < (1LL << 31) &&
                  ((M - 1) * x_row_stride + K) * esz < (1LL << 31),
              "lc_decode_linear: weight or x spans 2 GiB or more");
-  const int64_t out_cols = dl_out_cols(mode);
-  const int64_t n_blocks = (N + out_cols - 1) / out_cols;
-  LC_REQUIRE(n_blocks <= kDlMaxBlocks, "lc_decode_linear: N=%lld too large", (long long)N);
-  const int k_tiles = (int)(K / kDlKc);
-  const int s = dl_splits((int)n_blocks, k_tiles, splits, dl_n_cu());
-  const int64_t need = lc_decode_linear_workspace_bytes(M, N, K, mode, splits);
-  LC_REQUIRE(workspace_bytes >= need, "lc_decode_linear: workspace %lld < %lld bytes",
-             (long long)workspace_bytes, (long long)need);
+  DlPlan p;
+  LC_REQUIRE(dl_plan(N, K, mode, splits, &p), "lc_decode_linear: N=%lld too large", (long long)N);
+  // Unit indices and the owner arithmetic ((u + 1) * grid) stay in 64 bits;
+  // the unit count itself must fit an int.
+  LC_REQUIRE(p.n_blocks * p.k_tiles < (1LL << 31), "lc_decode_linear: too many tiles");
+  LC_REQUIRE(workspace_bytes >= p.workspace, "lc_decode_linear: workspace %lld < %lld bytes",
+             (long long)workspace_bytes, (long long)p.workspace);
   DlArgs a{};
   a.x = x;
   a.w = weight;
@@ -407,20 +497,28 @@ int lc_decode_linear(const void* x, int64_t x_row_stride, const void* weight,
   a.M = (int)M;
   a.K = (int)K;
   a.N = (int)N;
-  a.tiles_per_split = (k_tiles + s - 1) / s;
-  a.splits = s;
+  a.kt = (int)p.k_tiles;
+  a.n_blocks = (int)p.n_blocks;
   hipStream_t st = lc_stream(stream);
-  const dim3 grid((unsigned)n_blocks, (unsigned)s);
-  if (dtype == LC_DTYPE_BF16) {
-    if (mode == 0)
-      decode_linear_kernel<bf16_t, 0><<<grid, 64 * kDlWaves, 0, st>>>(a);
-    else
-      decode_linear_kernel<bf16_t, 1><<<grid, 64 * kDlWaves, 0, st>>>(a);
+  const dim3 grid((unsigned)p.grid);
+  const bool bf = dtype == LC_DTYPE_BF16;
+  const dim3 block(64 * kDlWaves);
+  if (p.rows == 64) {
+    if (mode == 0) {
+      if (bf) decode_linear_kernel<bf16_t, 0, 64><<<grid, block, 0, st>>>(a);
+      else decode_linear_kernel<f16_t, 0, 64><<<grid, block, 0, st>>>(a);
+    } else {
+      if (bf) decode_linear_kernel<bf16_t, 1, 64><<<grid, block, 0, st>>>(a);
+      else decode_linear_kernel<f16_t, 1, 64><<<grid, block, 0, st>>>(a);
+    }
   } else {
-    if (mode == 0)
-      decode_linear_kernel<f16_t, 0><<<grid, 64 * kDlWaves, 0, st>>>(a);
-    else
-      decode_linear_kernel<f16_t, 1><<<grid, 64 * kDlWaves, 0, st>>>(a);
+    if (mode == 0) {
+      if (bf) decode_linear_kernel<bf16_t, 0, 128><<<grid, block, 0, st>>>(a);
+      else decode_linear_kernel<f16_t, 0, 128><<<grid, block, 0, st>>>(a);
+    } else {
+      if (bf) decode_linear_kernel<bf16_t, 1, 128><<<grid, block, 0, st>>>(a);
+      else decode_linear_kernel<f16_t, 1, 128><<<grid, block, 0, st>>>(a);
+    }
   }
   return lc_check_launch("lc_decode_linear");
 }

@@ -50,7 +50,7 @@ constexpr int kLhStages = 3;            // LDS ring depth: two tiles in flight
 // once; streaming it past the caches measured 11% faster (230 -> 207 us at
 // the Llama-3-8B vocab) than the default policy. The hidden rows, re-read by
 // every workgroup, keep the default policy.
-constexpr int kLhWeightAux = 2;
+constexpr bool kLhWeightNt = true;
 constexpr int kLhBatch = 32;            // hidden rows per launch
 constexpr int kLhGenRows = 256;         // vocab rows per generic workgroup
 
@@ -171,8 +171,10 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
     else return (LC_LDS char*)h2;
   };
   auto fetch = [&](int t, auto st_c) __attribute__((always_inline)) {
-    pf_dma_tile<NIW_W, RPI, ROW_B, kLhWeightAux>(wbase, wbytes, wbuf(st_c), wave_s, woff, t * ROW_B);
-    pf_dma_tile<NIW_H, RPI, ROW_B>(a.hidden, hbytes, hbuf(st_c), wave_s, hoff, t * ROW_B);
+    pf_dma_tile_untracked<NIW_W, RPI, ROW_B, kLhWeightNt>(wbase, wbytes, wbuf(st_c), wave_s, woff,
+                                                   t * ROW_B);
+    pf_dma_tile_untracked<NIW_H, RPI, ROW_B, false>(a.hidden, hbytes, hbuf(st_c), wave_s, hoff,
+                                                    t * ROW_B);
   };
 
   f32x16_t acc[2];

@@ -497,7 +497,8 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False,
     x's dtype. swiglu=True: weight is [gate; up] ([2N, K]) and the result is
     swiglu(x @ gate.T, x @ up.T) with both projections rounded first (the
     reference's gate_proj / up_proj outputs). x: [..., K] with at most 32 rows.
-    splits: K-splits (0 = the library's choice).
+    splits: workgroups per row block of the weight (0 = the library's choice:
+    equal shares of the weight's tiles, one workgroup per CU).
     """
     if _records_grad(x, weight):
         raise RuntimeError("decode_linear is inference-only (autograd is recording)")

@@ -53,12 +53,21 @@ def test_decode_linear_arguments_rejected_before_launch():
     from llm_cuda import _native
 
     lib = _native.load()
-    assert lib.lc_decode_linear_counter_count(4096, 0) == 32
-    assert lib.lc_decode_linear_counter_count(14336, 1) == 224
+    # one counter per row block of the smaller shape (64 rows; 32 output
+    # columns in mode 1)
+    assert lib.lc_decode_linear_counter_count(4096, 0) == 64
+    assert lib.lc_decode_linear_counter_count(14336, 1) == 448
     assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 2, 0) == -1
-    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 0, 1) == 256  # unsplit
-    # one fp32 partial of 128 x 32 values per (row block, split)
-    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 0, 8) == 32 * 8 * 4096 * 4
+    # one workgroup per row block: no partials
+    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 0, 1) == 256
+    # K % 256 == 0: 64-row blocks of 16 tiles, 8 workgroups each; two fp32
+    # partials of 64 x 32 values per workgroup (its first and last block)
+    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4096, 0, 8) == 64 * 8 * 2 * 2048 * 4
+    # K % 256 == 128: 128-row blocks of 33 tiles, 3 workgroups each
+    assert lib.lc_decode_linear_workspace_bytes(32, 4096, 4224, 0, 3) == 32 * 3 * 2 * 4096 * 4
+    # the library's grid with 512 one-tile blocks: runs of two whole blocks,
+    # no partials (256 CUs where no GPU is visible)
+    assert lib.lc_decode_linear_workspace_bytes(1, 32768, 256, 0, 0) == 256
     for M, K, mode, what in ((33, 512, 0, b"M=33"), (4, 500, 0, b"multiple of 128"),
                              (4, 512, 3, b"mode 3")):
         rc = lib.lc_decode_linear(16, K, 16, K, 16, 256, M, 256, K, mode, 0, 16, 1 << 20, 16, 2,

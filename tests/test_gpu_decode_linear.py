@@ -75,6 +75,34 @@ def test_swiglu_matches_oracle(dtype, M, N, K, splits):
     _check(y, _ref(x, w, True), 3.0)
 
 
+@pytest.mark.parametrize("swiglu,M,N,K,splits", [
+    # 64-row blocks (K % 256 == 0), runs of 1-2 tiles that start and end
+    # inside blocks
+    (False, 32, 1000, 1280, 3),
+    # 128-row blocks (K % 256 == 128), runs of 1-2 tiles
+    (False, 9, 1000, 1152, 5),
+    # mode 1 with 64-row blocks: runs of 4-5 tiles over 9-tile blocks
+    (True, 32, 200, 2304, 2),
+    # mode 1 with 128-row blocks
+    (True, 7, 100, 384, 2),
+    # a workgroup per tile: every block summed from all its tiles' partials
+    (False, 4, 300, 3328, 13),
+    # the library's grid on 256 CUs: 313 blocks of 5 tiles in runs of 7, so
+    # a run can hold a whole block between two partial ones
+    (False, 16, 20000, 1280, 0),
+])
+def test_runs_across_row_blocks(swiglu, M, N, K, splits):
+    """Workgroup runs (equal shares of the (row block, K tile) units) that
+    start and end inside row blocks, so blocks are summed from the partials of
+    several workgroups, in both tile shapes and both modes."""
+    from llm_cuda.kernels import _ops
+
+    x, w = _inputs(M, N, K, torch.bfloat16, swiglu, seed=M * 7 + N + K)
+    y = _ops.decode_linear(x, w, swiglu=swiglu, splits=splits)
+    _check(y, _ref(x, w, swiglu), 3.0 if swiglu else 1.0)
+    assert torch.equal(y, _ops.decode_linear(x, w, swiglu=swiglu, splits=splits))
+
+
 def test_leading_dims_and_strided_rows():
     """x [B, 1, K] (the decode step's hidden states) and x rows with a stride
     past K (a column slice of a wider tensor)."""
