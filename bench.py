@@ -503,24 +503,6 @@ def run_model(args):
         layer.key_pages.normal_(generator=gd)
         layer.value_pages.normal_(generator=gd)
     ids = torch.randint(0, cfg.vocab_size, (B, 1), generator=gd, device=dev)
-    if args.tune_gemms:
-        # The q/k/v and o projections stay torch matmuls (the MLP's run on
-        # lc_decode_linear); PyTorch's TunableOp picks the fastest hipBLASLt /
-        # rocBLAS solution per shape during the first eager step. A 1 GB
-        # rotating buffer keeps the weights out of the 256 MB Infinity Cache
-        # while it times them, as in the real step. Tuning is switched off
-        # again before the graph is captured.
-        import tempfile
-
-        tun = torch.cuda.tunable
-        tun.set_filename(os.path.join(tempfile.gettempdir(), f"lcuda_tunableop_{os.getpid()}.csv"))
-        tun.set_rotating_buffer_size(1024)
-        if args.gemm_tuning_ms:
-            tun.set_max_tuning_duration(args.gemm_tuning_ms)
-            tun.set_max_tuning_iterations(100000)
-        tun.enable(True)
-        tun.tuning_enable(True)
-
     def reset():
         cache.seq_lens_all.fill_(ctx)
         for layer in cache.layer_caches:
@@ -535,13 +517,6 @@ def run_model(args):
         reset()
         eager_ids, eager_logits = step()
         eager_logits = eager_logits.float().clone()
-        if args.tune_gemms:
-            torch.cuda.tunable.tuning_enable(False)
-            try:
-                for r in torch.cuda.tunable.get_results():
-                    log("TunableOp pick: " + " | ".join(str(f) for f in r)[:220])
-            except Exception as exc:  # diagnostics only
-                log(f"TunableOp results unavailable: {exc}")
         # warm the allocator on a side stream, then capture
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -583,9 +558,8 @@ def run_model(args):
                    "batch": B, "context": ctx, "page_size": P, "layers": cfg.num_hidden_layers,
                    "hidden": cfg.hidden_size, "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size,
                    "hip_graph": True, "bytes_per_step": weights + kv,
-                   "projections": "q/k/v and o: torch matmul" + (
-                       " (TunableOp-selected hipBLASLt/rocBLAS solutions)" if args.tune_gemms
-                       else "") + "; gate/up + SwiGLU and down: native lc_decode_linear"},
+                   "projections": "native lc_decode_linear: fused q/k/v, o, gate/up + "
+                                  "SwiGLU, down"},
         "roofline": {"bound": "hbm", "kernel": "whole decode step (weights + KV read once)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -792,11 +766,6 @@ def main() -> int:
                                  "rmsnorm", "swiglu", "rope"])
     parser.add_argument("--split-tokens", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-gemm-tuning", dest="tune_gemms", action="store_false",
-                        help="model8b: keep torch's default GEMM solutions (no TunableOp)")
-    parser.add_argument("--gemm-tuning-ms", type=int, default=0,
-                        help="model8b: TunableOp's time budget per candidate solution (ms; "
-                             "0 = torch's default)")
     parser.add_argument("--prefill-shape", default=None, metavar="B,Hq,Hkv,S,D",
                         help="prefill: another shape instead of config 3 (4,32,8,4096,128)")
     parser.add_argument("--no-secondary", dest="secondary", action="store_false",

@@ -32,6 +32,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from llm_cuda.kernels import _ops
 from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
 from llm_cuda.kernels.triton.decode_attention import (
     paged_decode_attention,
@@ -115,7 +116,8 @@ class Llama3Attention(nn.Module):
 
         if FusedLinearWeights.usable(self.q_proj, self.k_proj, self.v_proj):
             nq, nk, _ = self._qkv.sizes()
-            qkv = F.linear(x, self._qkv.weight())
+            w = self._qkv.weight()
+            qkv = _ops.decode_linear(x, w) if _ops.decode_linear_applies(x, w) else F.linear(x, w)
             q = self._shape(qkv[..., :nq], self.num_heads)
             k = self._shape(qkv[..., nq:nq + nk], self.num_kv_heads)
             v = self._shape(qkv[..., nq + nk:], self.num_kv_heads)
@@ -151,6 +153,9 @@ class Llama3Attention(nn.Module):
                     q, cache.key_pages, cache.value_pages, cache.block_table, cache.seq_lens,
                     attention_mask=attention_mask, uniform_length=cache.uniform_length)
             out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
+            wo = self.o_proj.weight
+            if _ops.decode_linear_applies(out, wo):
+                return _ops.decode_linear(out, wo), cache
             return self.o_proj(out), cache
 
         cos, sin = self._rope_tables(past_len, seq_len, x.device, x.dtype)
