@@ -8,8 +8,9 @@ sequences, inputs resident in HBM. `value` = algorithmic bytes / step time.
 
 Other workloads (--workload): decode70b (config 5), prefill (config 3,
 TFLOP/s), prefill_bwd (the attention backward at the config-3 shape), lm_head
-(fused lm_head + greedy argmax at the config-4 vocab), decode_linear (the
-decode-step MLP projections on lc_decode_linear at the config-4 shape),
+(fused lm_head + greedy argmax at the config-4 vocab), decode_linear (one
+decoder layer's decode-step projections on lc_decode_linear at the config-4
+shape),
 model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
 swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
 (counter calibration copy).
@@ -382,70 +383,82 @@ def run_lm_head(args):
 
 
 def run_decode_linear(args):
-    """Decode-step MLP projections at the config-4 shape (32 rows): gate/up +
-    SwiGLU ([2 x 14336, 4096] weight, lc_decode_linear mode 1) followed by down
-    ([4096, 14336], mode 0), the reference's mlp.py:39-43 at a decode step."""
+    """The four weight projections of one decoder layer's decode step at the
+    config-4 shape (32 rows), each one lc_decode_linear launch: fused q/k/v
+    ([6144, 4096], the reference's attention.py:100-102), o ([4096, 4096],
+    attention.py:154), gate/up + SwiGLU ([2 x 14336, 4096], mode 1, mlp.py:39-43)
+    and down ([4096, 14336], mode 0)."""
     import torch
     import torch.nn.functional as F
 
     from llm_cuda.kernels import _ops
 
     dev = torch.device("cuda", 0)
-    M, H, FF = 32, 4096, 14336
+    M, H, FF, QKV = 32, 4096, 14336, 6144
     g = torch.Generator(device=dev).manual_seed(0)
-    # Four weight sets (1.4 GB) in rotation, so no step finds its weights in
+
+    def weight(n, k):
+        return (torch.randn(n, k, generator=g, device=dev) * k ** -0.5).bfloat16()
+
+    # Four weight sets (1.7 GB) in rotation, so no step finds its weights in
     # the 256 MB Infinity Cache (in the model each layer's weights are cold).
-    sets = [((torch.randn(2 * FF, H, generator=g, device=dev) * H ** -0.5).bfloat16(),
-             (torch.randn(H, FF, generator=g, device=dev) * FF ** -0.5).bfloat16())
-            for _ in range(4)]
+    sets = [(weight(QKV, H), weight(H, H), weight(2 * FF, H), weight(H, FF)) for _ in range(4)]
     x = torch.randn(M, H, generator=g, device=dev).bfloat16()
+    attn = torch.randn(M, H, generator=g, device=dev).bfloat16()
     state = {"i": 0}
 
     def step():
         state["i"] = (state["i"] + 1) % len(sets)
-        wgu, wd = sets[state["i"]]
-        return _ops.decode_linear(_ops.decode_linear(x, wgu, swiglu=True), wd)
+        wqkv, wo, wgu, wd = sets[state["i"]]
+        return (_ops.decode_linear(x, wqkv), _ops.decode_linear(attn, wo),
+                _ops.decode_linear(_ops.decode_linear(x, wgu, swiglu=True), wd))
 
     ms, wall = time_steps(step, args.steps, args.warmup)
-    nbytes = 3 * FF * H * 2 + M * (H + FF + H) * 2
+    wbytes = (QKV * H + H * H + 3 * FF * H) * 2
+    nbytes = wbytes + M * (H + QKV + H + H + H + FF + FF + H) * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
 
     def torch_step():
         state["i"] = (state["i"] + 1) % len(sets)
-        wgu, wd = sets[state["i"]]
+        wqkv, wo, wgu, wd = sets[state["i"]]
         gu = F.linear(x, wgu)
-        return F.linear(_ops.swiglu(gu[:, :FF], gu[:, FF:]), wd)
+        return (F.linear(x, wqkv), F.linear(attn, wo),
+                F.linear(_ops.swiglu(gu[:, :FF], gu[:, FF:]), wd))
 
     ms_t, _ = time_steps(torch_step, args.steps, args.warmup)
-    log(f"decode_linear: {ms * 1e3:.1f} us/step (gate/up + SwiGLU + down), {gbs:.0f} GB/s "
-        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM); torch linear + SwiGLU kernel + linear "
-        f"(default solutions): {ms_t * 1e3:.1f} us")
+    log(f"decode_linear: {ms * 1e3:.1f} us/step (q/k/v, o, gate/up + SwiGLU, down), "
+        f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM); torch linears + SwiGLU "
+        f"kernel (default solutions): {ms_t * 1e3:.1f} us")
     result = {
-        "metric": "decode MLP projections GB/s",
+        "metric": "decode-step projections GB/s",
         "value": round(gbs, 1),
         "unit": "GB/s",
         "ms_per_step": round(ms, 5),
         "dtype": "bf16",
-        "config": {"workload": "decode-step MLP (gate/up + SwiGLU, down), Llama-3-8B shapes at "
-                               "batch 32 (BASELINE config 4 layer)", "rows": M, "hidden": H,
-                   "ffn": FF, "bytes_per_step": nbytes, "torch_ms": round(ms_t, 5)},
-        "roofline": {"bound": "hbm", "kernel": "decode_linear_kernel (2 launches)",
+        "config": {"workload": "one decoder layer's decode-step projections (q/k/v, o, gate/up "
+                               "+ SwiGLU, down), Llama-3-8B shapes at batch 32 (BASELINE "
+                               "config 4 layer)", "rows": M, "hidden": H, "ffn": FF,
+                   "bytes_per_step": nbytes, "torch_ms": round(ms_t, 5)},
+        "roofline": {"bound": "hbm", "kernel": "decode_linear_kernel (4 launches)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("decode_linear_mlp_8b")},
+                     "traffic": measured_traffic("decode_linear_layer_8b")},
     }
     if not args.no_cpu_baseline:
         from oracle.elementwise import swiglu
         from oracle.lm_head import lm_head_logits
 
         torch.set_num_threads(cpu_threads())
-        xs = x.cpu()
-        wgu, wd = (w.cpu() for w in sets[0])
+        xs, attn_s = x.cpu(), attn.cpu()
+        wqkv, wo, wgu, wd = (w.cpu() for w in sets[0])
         # 1/8 of the output columns of each projection (a bounded sample)
         cols = FF // 8
         wg_s, wu_s, wd_s = wgu[:cols], wgu[FF:FF + cols], wd[:H // 8]
+        wqkv_s, wo_s = wqkv[:QKV // 8], wo[:H // 8]
 
         def cpu_step():
+            lm_head_logits(xs, wqkv_s)
+            lm_head_logits(attn_s, wo_s)
             h = swiglu(lm_head_logits(xs, wg_s), lm_head_logits(xs, wu_s)).bfloat16()
             hfull = torch.zeros(M, FF, dtype=torch.bfloat16)
             hfull[:, :cols] = h

@@ -4,7 +4,9 @@ Same module, parameters and call signature as the reference. The forward pass
 differs only in how the attention itself is computed, all on HIP kernels:
 
   * Inference projections: q, k and v come out of one GEMM against the
-    concatenated weight (the parameters alias its row blocks).
+    concatenated weight (the parameters alias its row blocks). With at most
+    32 rows (a decode step) that GEMM and o_proj are native launches that
+    stream the weight once (`decode_linear`).
   * RoPE: Q and K rotated in one launch, reading the transposed projection
     views directly. The cos/sin tables are built once for a range of
     positions and sliced per call (every row depends only on its position,
