@@ -74,6 +74,23 @@ LC_API int lc_add_rmsnorm_fwd(const void* x, const void* residual, const void* w
                        int64_t r_row_stride, int64_t y_row_stride, int64_t s_row_stride,
                        float eps, int dtype, int w_dtype, void* stream);
 
+/* lc_add_rmsnorm_fwd with the residual addend given as n_partials fp32
+ * partial sums left by lc_decode_linear_partials: residual = round(0.0f +
+ * p_0 + p_1 + ... + p_{n-1}) elementwise, summed in that order and rounded to
+ * dtype (the value lc_decode_linear would have written), then s = x +
+ * residual, sum_out = s, y = rmsnorm(s) * w. It replaces the same reference
+ * pair as lc_add_rmsnorm_fwd (models/llama3/model.py:29-42) when the
+ * projection before it (o_proj, down_proj) leaves its split-K sum to it.
+ * Partial p of row r: partials + p * partial_stride + r * p_row_stride (fp32
+ * elements). sum_out may be x; y must not alias x or sum_out. 1 <= n_partials
+ * <= 1024. */
+LC_API int lc_add_rmsnorm_partials_fwd(const void* x, const float* partials, int64_t n_partials,
+                                       int64_t partial_stride, const void* w, void* y,
+                                       void* sum_out, int64_t rows, int64_t hidden,
+                                       int64_t x_row_stride, int64_t p_row_stride,
+                                       int64_t y_row_stride, int64_t s_row_stride, float eps,
+                                       int dtype, int w_dtype, void* stream);
+
 /* SwiGLU forward: out = silu(gate) * up = gate * sigmoid(gate) * up (fp32 math).
  * Replaces csrc/rmsnorm_extension.cpp:25-40 (swiglu_forward),
  * csrc/swiglu_kernel.cu:7-57 and kernels/triton/swiglu.py:15-42,91-145.
@@ -213,6 +230,23 @@ LC_API int lc_decode_linear(const void* x, int64_t x_row_stride, const void* wei
                             int64_t weight_row_stride, void* y, int64_t y_row_stride, int64_t M,
                             int64_t N, int64_t K, int mode, int splits, void* workspace,
                             int64_t workspace_bytes, int* counters, int dtype, void* stream);
+
+/* Shares per row block lc_decode_linear_partials uses by default for an
+ * [N, K] weight (the number of partials it writes per output), or -1. */
+LC_API int64_t lc_decode_linear_partial_count(int64_t N, int64_t K);
+
+/* lc_decode_linear mode 0 with its split-K sum left to the consumer: each of
+ * `shares` equal K-shares of every row block (0 = the library's choice,
+ * lc_decode_linear_partial_count) writes its fp32 partial to
+ * partials[(s * M + m) * N + n], with no hand-off between workgroups (no
+ * workspace, no counters). round(0.0f + p_0 + ... + p_{shares-1}) equals
+ * lc_decode_linear's output. For the decode step's o_proj and down_proj
+ * (models/llama3/attention.py:154, mlp.py:35-37), whose sums
+ * lc_add_rmsnorm_partials_fwd adds. shares must divide the tiles of a row
+ * block; N % 4 == 0; partials 16-byte aligned, [shares, M, N] contiguous. */
+LC_API int lc_decode_linear_partials(const void* x, int64_t x_row_stride, const void* weight,
+                                     int64_t weight_row_stride, float* partials, int64_t M,
+                                     int64_t N, int64_t K, int shares, int dtype, void* stream);
 
 /* Bytes of fp32 workspace lc_paged_decode_fwd needs for these sizes
  * (partial outputs and logsumexps of every split). */

@@ -82,6 +82,10 @@ struct DlArgs {
   int M, K, N;         // N = output columns
   int kt;              // K tiles per row block
   int n_blocks;
+  // Partial output (OUTP): share s of every row block writes its fp32 sum to
+  // pout[(s * M + m) * N + n]; there are `shares` equal shares per block.
+  float* pout;
+  int shares;
 };
 
 // First unit of workgroup g's run when U units are dealt to G workgroups.
@@ -93,7 +97,7 @@ __device__ __forceinline__ int dl_owner(int64_t u, int64_t U, int64_t G) {
   return static_cast<int>(((u + 1) * G - 1) / U);
 }
 
-template <typename T, int MODE, int ROWS>
+template <typename T, int MODE, int ROWS, bool OUTP = false>
 __global__ __launch_bounds__(64 * kDlWaves) void decode_linear_kernel(DlArgs a) {
   typedef Mfma32<T> Ops;
   typedef typename Ops::v8 v8;
@@ -228,6 +232,25 @@ __global__ __launch_bounds__(64 * kDlWaves) void decode_linear_kernel(DlArgs a) 
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[0][r] += xk[(rw * 16 + r) * 64 + lane];
       }
+    }
+    if constexpr (OUTP) {
+      // The grid is n_blocks x shares workgroups, one share each (block g /
+      // shares, share g % shares): the share's fp32 sum goes out as it is,
+      // for the consumer to add up. Holding lane (l32, hh) of row group rw:
+      // x row l32, columns rw*32 + 8j + 4hh + i (register 4j + i). N % 4 == 0.
+      if (!holder || l32 >= a.M) return;
+      const int c0 = blk * OUTC;
+      const int cols_valid = min(OUTC, a.N - c0);
+      float* prow = a.pout + ((int64_t)(g % a.shares) * a.M + l32) * a.N + c0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = rw * 32 + j * 8 + hh * 4;
+        if (col < cols_valid) {
+          const f32x4_t v = {acc[0][4 * j], acc[0][4 * j + 1], acc[0][4 * j + 2], acc[0][4 * j + 3]};
+          *reinterpret_cast<f32x4_t*>(prow + col) = v;
+        }
+      }
+      return;
     }
     const int blk_lo = blk * kt;
     const int run_lo = u_begin;
@@ -420,6 +443,20 @@ int dl_n_cu() {
 // tiles, else 128.
 int dl_rows(int64_t K) { return K % (2 * kDlKc) == 0 ? 64 : 128; }
 
+// Shares per row block for partial output. Where lc_decode_linear's own grid
+// deals each block out in equal whole shares, the same shares (so the two
+// paths add the same partials in the same order); otherwise the fewest that
+// divide the block's tiles and keep at least 3/4 of the CUs busy (every share
+// is one workgroup), else one per tile.
+int64_t dl_shares(int64_t n_blocks, int64_t k_tiles, int n_cu) {
+  const int64_t U = n_blocks * k_tiles;
+  const int64_t g = dl_grid(n_blocks, k_tiles, 0, n_cu);
+  if (U % g == 0 && k_tiles % (U / g) == 0) return k_tiles / (U / g);
+  for (int64_t d = 1; d <= k_tiles; ++d)
+    if (k_tiles % d == 0 && 4 * n_blocks * d >= 3 * (int64_t)n_cu) return d;
+  return k_tiles;
+}
+
 struct DlPlan {
   int rows;
   int64_t n_blocks, k_tiles, grid, workspace;
@@ -529,6 +566,69 @@ int lc_decode_linear(const void* x, int64_t x_row_stride, const void* weight,
     }
   }
   return lc_check_launch("lc_decode_linear");
+}
+
+int64_t lc_decode_linear_partial_count(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % kDlKc) return -1;
+  const int rows = dl_rows(K);
+  const int64_t n_blocks = (N + rows - 1) / rows;
+  if (n_blocks > kDlMaxBlocks) return -1;
+  return dl_shares(n_blocks, K / (kDlTileElems / rows), dl_n_cu());
+}
+
+int lc_decode_linear_partials(const void* x, int64_t x_row_stride, const void* weight,
+                              int64_t weight_row_stride, float* partials, int64_t M, int64_t N,
+                              int64_t K, int shares, int dtype, void* stream) {
+  LC_REQUIRE(dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16,
+             "lc_decode_linear_partials: dtype %d (bf16 or f16 only)", dtype);
+  LC_REQUIRE(M >= 0 && M <= kDlBatch, "lc_decode_linear_partials: M=%lld rows (1..%d)",
+             (long long)M, kDlBatch);
+  if (M == 0) return LC_OK;
+  LC_REQUIRE(x && weight && partials, "lc_decode_linear_partials: null pointer");
+  LC_REQUIRE(N > 0 && K > 0 && K % kDlKc == 0 && K < (1LL << 30) && N < (1LL << 30) && N % 4 == 0,
+             "lc_decode_linear_partials: N=%lld K=%lld (K a positive multiple of %d, N of 4)",
+             (long long)N, (long long)K, kDlKc);
+  LC_REQUIRE(x_row_stride >= K && weight_row_stride >= K,
+             "lc_decode_linear_partials: row strides too small");
+  LC_REQUIRE(lc_aligned(x, 16) && lc_aligned(weight, 16) && x_row_stride % 8 == 0 &&
+                 weight_row_stride % 8 == 0,
+             "lc_decode_linear_partials: x and weight need 16-byte aligned rows");
+  LC_REQUIRE(lc_aligned(partials, 16), "lc_decode_linear_partials: partials not 16-byte aligned");
+  LC_REQUIRE(N * weight_row_stride * 2 < (1LL << 31) && ((M - 1) * x_row_stride + K) * 2 < (1LL << 31),
+             "lc_decode_linear_partials: weight or x spans 2 GiB or more");
+  const int rows = dl_rows(K);
+  const int64_t n_blocks = (N + rows - 1) / rows;
+  LC_REQUIRE(n_blocks <= kDlMaxBlocks, "lc_decode_linear_partials: N=%lld too large",
+             (long long)N);
+  const int64_t kt = K / (kDlTileElems / rows);
+  const int64_t s = shares > 0 ? shares : dl_shares(n_blocks, kt, dl_n_cu());
+  LC_REQUIRE(kt % s == 0, "lc_decode_linear_partials: %lld shares do not divide the %lld tiles "
+             "of a row block", (long long)s, (long long)kt);
+  LC_REQUIRE(n_blocks * kt < (1LL << 31), "lc_decode_linear_partials: too many tiles");
+  DlArgs a{};
+  a.x = x;
+  a.w = weight;
+  a.xs = x_row_stride;
+  a.ws = weight_row_stride;
+  a.M = (int)M;
+  a.K = (int)K;
+  a.N = (int)N;
+  a.kt = (int)kt;
+  a.n_blocks = (int)n_blocks;
+  a.pout = partials;
+  a.shares = (int)s;
+  hipStream_t st = lc_stream(stream);
+  const dim3 grid((unsigned)(n_blocks * s));
+  const dim3 block(64 * kDlWaves);
+  const bool bf = dtype == LC_DTYPE_BF16;
+  if (rows == 64) {
+    if (bf) decode_linear_kernel<bf16_t, 0, 64, true><<<grid, block, 0, st>>>(a);
+    else decode_linear_kernel<f16_t, 0, 64, true><<<grid, block, 0, st>>>(a);
+  } else {
+    if (bf) decode_linear_kernel<bf16_t, 0, 128, true><<<grid, block, 0, st>>>(a);
+    else decode_linear_kernel<f16_t, 0, 128, true><<<grid, block, 0, st>>>(a);
+  }
+  return lc_check_launch("lc_decode_linear_partials");
 }
 
 }  // extern "C"

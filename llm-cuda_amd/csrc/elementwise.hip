@@ -20,37 +20,104 @@ namespace {
 // per lane) so it is read from HBM once; ITEMS == 0 selects a two-pass loop
 // for rows too wide to cache (re-read hits L2).
 // Follows kernels/cuda/csrc/rmsnorm_kernel.cu:26-49: y = (x * inv_rms) * w.
-// ADD: the input row is s = x + r rounded to T (the decoder layer's residual
-// add, models/llama3/model.py:29-42), written to s_out and then normalised.
+// ADD 1: the input row is s = x + r rounded to T (the decoder layer's
+// residual add, models/llama3/model.py:29-42), written to s_out and then
+// normalised. ADD 2: the same with r = round(sum of np fp32 partials), the
+// partials of a projection whose sum was left to this kernel
+// (lc_decode_linear_partials): partial p of the row at pp + p * pss + row *
+// prs, added to 0.0f in order p = 0, 1, ... and rounded to T, as the
+// projection's own epilogue would have.
 // ---------------------------------------------------------------------------
-template <typename T, typename W, int VEC, int ITEMS, bool ADD>
+template <typename T, typename W, int VEC, int ITEMS, int ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __restrict__ w,
                                                       T* __restrict__ y, int hidden,
                                                       int64_t xs, int64_t ys, float eps,
                                                       const T* r, int64_t rs, T* s_out,
-                                                      int64_t ss) {
+                                                      int64_t ss, const float* pp, int64_t prs,
+                                                      int64_t pss, int np) {
   const int64_t row = blockIdx.x;
   // (x may alias s_out: every element is read by the thread that writes it)
   const T* xr = x + row * xs;
   T* yr = y + row * ys;
-  const T* rr = ADD ? r + row * rs : nullptr;
+  const T* rr = ADD == 1 ? r + row * rs : nullptr;
+  const float* pr = ADD == 2 ? pp + row * prs : nullptr;
   T* sr = ADD ? s_out + row * ss : nullptr;
   const int nvec = hidden / VEC;
   const int tid = threadIdx.x;
   const int nthreads = blockDim.x;
 
-  // Loads vector vi of the input row (x, or round(x + r)) as fp32.
+  // Addend vector vi (ADD 2): the partials summed in order, rounded to T.
+  // The first four partials are loaded by issue_parts (so a caller can issue
+  // several vectors' loads before the first sum); finish_parts adds them and
+  // any further partials, four loads at a time.
+  auto load_part = [&](int p, int vi, float (&t)[VEC]) __attribute__((always_inline)) {
+    const float* src = pr + (int64_t)p * pss + (int64_t)vi * VEC;
+    if constexpr (VEC % 4 == 0) {
+#pragma unroll
+      for (int q = 0; q < VEC / 4; ++q) {
+        const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(src + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[4 * q + e] = v4[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) t[e] = src[e];
+    }
+  };
+  auto issue_parts = [&](int vi, float (&t)[4][VEC]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < np) load_part(k, vi, t[k]);
+  };
+  auto finish_parts = [&](int vi, float (&t)[4][VEC], T (&out)[VEC]) __attribute__((always_inline)) {
+    float a[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) a[e] = 0.f;
+    for (int p0 = 0; p0 < np; p0 += 4) {
+      if (p0 > 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (p0 + k < np) load_part(p0 + k, vi, t[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (p0 + k < np) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) a[e] += t[k][e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[e] = lc_from_f32<T>(a[e]);
+  };
+  // Addend vector vi (ADD 1 or 2) in T.
+  auto load_addend = [&](int vi, T (&out)[VEC]) __attribute__((always_inline)) {
+    if constexpr (ADD == 2) {
+      float t[4][VEC];
+      issue_parts(vi, t);
+      finish_parts(vi, t, out);
+    } else if constexpr (VEC * sizeof(T) == 16) {
+      const Vec16<T> b = EW_LD(rr + (int64_t)vi * VEC);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) out[e] = b.v[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) out[e] = rr[(int64_t)vi * VEC + e];
+    }
+  };
+
+  // Loads vector vi of the input row (x, or round(x + addend)) as fp32.
   auto load_row = [&](int vi, float (&v)[VEC]) {
+    T add[VEC];
+    if constexpr (ADD != 0) load_addend(vi, add);
     if constexpr (VEC * sizeof(T) == 16) {
       Vec16<T> a = EW_LD(xr + (int64_t)vi * VEC);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) v[e] = lc_to_f32(a.v[e]);
-      if constexpr (ADD) {
-        Vec16<T> b = EW_LD(rr + (int64_t)vi * VEC);
+      if constexpr (ADD != 0) {
         Vec16<T> sum;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          sum.v[e] = lc_from_f32<T>(v[e] + lc_to_f32(b.v[e]));
+          sum.v[e] = lc_from_f32<T>(v[e] + lc_to_f32(add[e]));
           v[e] = lc_to_f32(sum.v[e]);
         }
         EW_ST(sr + (int64_t)vi * VEC, sum);
@@ -60,8 +127,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
       for (int e = 0; e < VEC; ++e) {
         const int64_t c = (int64_t)vi * VEC + e;
         v[e] = lc_to_f32(xr[c]);
-        if constexpr (ADD) {
-          const T sum = lc_from_f32<T>(v[e] + lc_to_f32(rr[c]));
+        if constexpr (ADD != 0) {
+          const T sum = lc_from_f32<T>(v[e] + lc_to_f32(add[e]));
           sr[c] = sum;
           v[e] = lc_to_f32(sum);
         }
@@ -79,6 +146,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
     // (which x may alias), with no branch between them (items past the row
     // re-read its last vector), so the items cost one memory round trip.
     T xraw[ITEMS][VEC], rraw[ITEMS][VEC];
+    float praw[ADD == 2 ? ITEMS : 1][4][VEC];
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int vi = min(tid + it * nthreads, nvec - 1);
@@ -88,18 +156,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
         const Vec16<T> a = EW_LD(xr + (int64_t)vi * VEC);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) xraw[it][e] = a.v[e];
-        if constexpr (ADD) {
-          const Vec16<T> b = EW_LD(rr + (int64_t)vi * VEC);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) rraw[it][e] = b.v[e];
-        }
       } else {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          xraw[it][e] = xr[(int64_t)vi * VEC + e];
-          if constexpr (ADD) rraw[it][e] = rr[(int64_t)vi * VEC + e];
-        }
+        for (int e = 0; e < VEC; ++e) xraw[it][e] = xr[(int64_t)vi * VEC + e];
       }
+      if constexpr (ADD == 1) load_addend(vi, rraw[it]);
+      if constexpr (ADD == 2) issue_parts(vi, praw[it]);
+    }
+    if constexpr (ADD == 2) {
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it)
+        finish_parts(min(tid + it * nthreads, nvec - 1), praw[it], rraw[it]);
     }
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
@@ -110,7 +177,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         float v = lc_to_f32(xraw[it][e]);
-        if constexpr (ADD) {
+        if constexpr (ADD != 0) {
           const T sv = lc_from_f32<T>(v + lc_to_f32(rraw[it][e]));
           sum.v[e % Vec16<T>::N] = sv;
           v = lc_to_f32(sv);
@@ -119,7 +186,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
         sq = fmaf(v, v, sq);
       }
       acc += live ? sq : 0.f;
-      if constexpr (ADD) {
+      if constexpr (ADD != 0) {
         if (live) {
           if constexpr (VEC * sizeof(T) == 16) {
             EW_ST(sr + (int64_t)vi * VEC, sum);
@@ -185,10 +252,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, const W* __res
   }
 }
 
-template <typename T, typename W, int VEC, bool ADD>
+// Addend of ADD 2: np fp32 partials, partial p of row r at pp + p * pss + r * prs.
+struct RmsParts {
+  const float* pp = nullptr;
+  int64_t prs = 0, pss = 0;
+  int np = 0;
+};
+
+template <typename T, typename W, int VEC, int ADD>
 int launch_rmsnorm_vec(const T* x, const W* w, T* y, int64_t rows, int64_t hidden, int64_t xs,
                        int64_t ys, float eps, const T* r, int64_t rs, T* s_out, int64_t ss,
-                       hipStream_t st) {
+                       RmsParts pt, hipStream_t st) {
   const int64_t nvec = hidden / VEC;
   int threads = static_cast<int>(lc_cdiv(nvec, 64) * 64);
   if (threads > 256) threads = 256;
@@ -197,7 +271,8 @@ int launch_rmsnorm_vec(const T* x, const W* w, T* y, int64_t rows, int64_t hidde
   dim3 grid(static_cast<unsigned>(rows));
 #define LC_RMS(ITEMS)                                                                       \
   rmsnorm_kernel<T, W, VEC, ITEMS, ADD><<<grid, threads, 0, st>>>(x, w, y, (int)hidden, xs, \
-                                                                  ys, eps, r, rs, s_out, ss)
+                                                                  ys, eps, r, rs, s_out, ss, \
+                                                                  pt.pp, pt.prs, pt.pss, pt.np)
   if (items <= 1)
     LC_RMS(1);
   else if (items <= 2)
@@ -209,48 +284,52 @@ int launch_rmsnorm_vec(const T* x, const W* w, T* y, int64_t rows, int64_t hidde
   else
     LC_RMS(0);
 #undef LC_RMS
-  return lc_check_launch(ADD ? "lc_add_rmsnorm_fwd" : "lc_rmsnorm_fwd");
+  return lc_check_launch(ADD == 2 ? "lc_add_rmsnorm_partials_fwd"
+                                  : ADD ? "lc_add_rmsnorm_fwd" : "lc_rmsnorm_fwd");
 }
 
-template <typename T, typename W, bool ADD>
+template <typename T, typename W, int ADD>
 int launch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
                    int64_t xs, int64_t ys, float eps, const void* r, int64_t rs, void* s_out,
-                   int64_t ss, hipStream_t st) {
+                   int64_t ss, RmsParts pt, hipStream_t st) {
   constexpr int V = 16 / sizeof(T);
   bool vec_ok = (hidden % V == 0) && (xs % V == 0) && (ys % V == 0) && lc_aligned(x, 16) &&
                 lc_aligned(y, 16);
-  if (ADD) vec_ok = vec_ok && rs % V == 0 && ss % V == 0 && lc_aligned(r, 16) && lc_aligned(s_out, 16);
+  if (ADD) vec_ok = vec_ok && ss % V == 0 && lc_aligned(s_out, 16);
+  if (ADD == 1) vec_ok = vec_ok && rs % V == 0 && lc_aligned(r, 16);
+  if (ADD == 2) vec_ok = vec_ok && pt.prs % 4 == 0 && pt.pss % 4 == 0 && lc_aligned(pt.pp, 16);
   if (vec_ok)
     return launch_rmsnorm_vec<T, W, V, ADD>(
         static_cast<const T*>(x), static_cast<const W*>(w), static_cast<T*>(y), rows, hidden, xs,
-        ys, eps, static_cast<const T*>(r), rs, static_cast<T*>(s_out), ss, st);
+        ys, eps, static_cast<const T*>(r), rs, static_cast<T*>(s_out), ss, pt, st);
   return launch_rmsnorm_vec<T, W, 1, ADD>(
       static_cast<const T*>(x), static_cast<const W*>(w), static_cast<T*>(y), rows, hidden, xs,
-      ys, eps, static_cast<const T*>(r), rs, static_cast<T*>(s_out), ss, st);
+      ys, eps, static_cast<const T*>(r), rs, static_cast<T*>(s_out), ss, pt, st);
 }
 
-template <bool ADD>
+template <int ADD>
 int dispatch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t hidden,
                      int64_t xs, int64_t ys, float eps, const void* r, int64_t rs, void* s_out,
-                     int64_t ss, int dtype, int w_dtype, hipStream_t st) {
+                     int64_t ss, RmsParts pt, int dtype, int w_dtype, hipStream_t st) {
   const bool wf = w_dtype == LC_DTYPE_F32;
   switch (dtype) {
     case LC_DTYPE_F32:
       return launch_rmsnorm<float, float, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs, s_out,
-                                               ss, st);
+                                               ss, pt, st);
     case LC_DTYPE_BF16:
       return wf ? launch_rmsnorm<bf16_t, float, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
-                                                     s_out, ss, st)
+                                                     s_out, ss, pt, st)
                 : launch_rmsnorm<bf16_t, bf16_t, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
-                                                      s_out, ss, st);
+                                                      s_out, ss, pt, st);
     case LC_DTYPE_F16:
       return wf ? launch_rmsnorm<f16_t, float, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
-                                                    s_out, ss, st)
+                                                    s_out, ss, pt, st)
                 : launch_rmsnorm<f16_t, f16_t, ADD>(x, w, y, rows, hidden, xs, ys, eps, r, rs,
-                                                    s_out, ss, st);
+                                                    s_out, ss, pt, st);
     default:
       return lc_fail(LC_EINVAL, "%s: unknown dtype %d",
-                     ADD ? "lc_add_rmsnorm_fwd" : "lc_rmsnorm_fwd", dtype);
+                     ADD == 2 ? "lc_add_rmsnorm_partials_fwd"
+                              : ADD ? "lc_add_rmsnorm_fwd" : "lc_rmsnorm_fwd", dtype);
   }
 }
 
@@ -497,8 +576,8 @@ int lc_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t 
   LC_REQUIRE(w_dtype == dtype || w_dtype == LC_DTYPE_F32,
              "lc_rmsnorm_fwd: weight dtype must equal x dtype or be fp32");
   if (rows == 0) return LC_OK;
-  return dispatch_rmsnorm<false>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, nullptr,
-                                 0, nullptr, 0, dtype, w_dtype, lc_stream(stream));
+  return dispatch_rmsnorm<0>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, nullptr, 0,
+                             nullptr, 0, RmsParts{}, dtype, w_dtype, lc_stream(stream));
 }
 
 int lc_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y,
@@ -515,9 +594,39 @@ int lc_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void*
   LC_REQUIRE(rows == 0 || (y != sum_out && y != x && y != residual),
              "lc_add_rmsnorm_fwd: y must not alias x, residual or sum_out");
   if (rows == 0) return LC_OK;
-  return dispatch_rmsnorm<true>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, residual,
-                                r_row_stride, sum_out, s_row_stride, dtype, w_dtype,
-                                lc_stream(stream));
+  return dispatch_rmsnorm<1>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, residual,
+                             r_row_stride, sum_out, s_row_stride, RmsParts{}, dtype, w_dtype,
+                             lc_stream(stream));
+}
+
+int lc_add_rmsnorm_partials_fwd(const void* x, const float* partials, int64_t n_partials,
+                                int64_t partial_stride, const void* w, void* y, void* sum_out,
+                                int64_t rows, int64_t hidden, int64_t x_row_stride,
+                                int64_t p_row_stride, int64_t y_row_stride, int64_t s_row_stride,
+                                float eps, int dtype, int w_dtype, void* stream) {
+  LC_REQUIRE(rows >= 0 && hidden > 0,
+             "lc_add_rmsnorm_partials_fwd: bad shape rows=%lld hidden=%lld", (long long)rows,
+             (long long)hidden);
+  LC_REQUIRE(hidden < (1LL << 31) && rows < (1LL << 31),
+             "lc_add_rmsnorm_partials_fwd: shape too large");
+  LC_REQUIRE(n_partials >= 1 && n_partials <= 1024,
+             "lc_add_rmsnorm_partials_fwd: %lld partials (1..1024)", (long long)n_partials);
+  LC_REQUIRE((x && partials && w && y && sum_out) || rows == 0,
+             "lc_add_rmsnorm_partials_fwd: null pointer");
+  LC_REQUIRE(p_row_stride >= hidden && partial_stride >= 0,
+             "lc_add_rmsnorm_partials_fwd: partial strides too small");
+  LC_REQUIRE(w_dtype == dtype || w_dtype == LC_DTYPE_F32,
+             "lc_add_rmsnorm_partials_fwd: weight dtype must equal x dtype or be fp32");
+  LC_REQUIRE(rows == 0 || (y != sum_out && y != x),
+             "lc_add_rmsnorm_partials_fwd: y must not alias x or sum_out");
+  if (rows == 0) return LC_OK;
+  RmsParts pt;
+  pt.pp = partials;
+  pt.prs = p_row_stride;
+  pt.pss = partial_stride;
+  pt.np = (int)n_partials;
+  return dispatch_rmsnorm<2>(x, w, y, rows, hidden, x_row_stride, y_row_stride, eps, nullptr, 0,
+                             sum_out, s_row_stride, pt, dtype, w_dtype, lc_stream(stream));
 }
 
 int lc_swiglu_fwd(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,

@@ -79,6 +79,17 @@ _SIGNATURES = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int,
          ctypes.c_int, _c_p, _c_i64, _c_p, ctypes.c_int, _c_p],
     ),
+    "lc_decode_linear_partial_count": (_c_i64, [_c_i64, _c_i64]),
+    "lc_decode_linear_partials": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+         _c_p],
+    ),
+    "lc_add_rmsnorm_partials_fwd": (
+        ctypes.c_int,
+        [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, ctypes.c_float, ctypes.c_int, ctypes.c_int, _c_p],
+    ),
     "lc_paged_decode_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "lc_paged_decode_fwd": (
         ctypes.c_int,

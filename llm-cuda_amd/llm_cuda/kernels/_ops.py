@@ -113,14 +113,20 @@ def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor
     return y.view(x.shape)
 
 
-def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+def add_rms_norm(x: torch.Tensor, residual, weight: torch.Tensor, eps: float,
                  inplace: bool = False):
     """s = x + residual (rounded to x's dtype), y = rms_norm(s) * weight; returns (y, s).
 
     One pass over the rows instead of an add and a norm (reference pair:
     models/llama3/model.py:29-42). With inplace=True, s is written into x.
+    residual may be a PartialSum (a projection's split-K partials, see
+    decode_linear_partials): its sum is formed in the same pass.
     Forward only: a backward through y or s raises.
     """
+    if isinstance(residual, PartialSum):
+        if _records_grad(x, weight):
+            raise NotImplementedError("add_rms_norm over partial sums is forward-only")
+        return _add_rms_norm_partials(x, residual, weight, eps, inplace)
     if _records_grad(x, residual, weight):
         if inplace:
             raise NotImplementedError(
@@ -159,6 +165,36 @@ def _add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
             hidden, x2.stride(0), r2.stride(0), y.stride(0), s2.stride(0), float(eps),
             nat.lc_dtype(x), nat.lc_dtype(w), _stream(dev))
     nat.check(rc, "lc_add_rmsnorm_fwd")
+    return y.view(x.shape), (x if inplace else s2.view(x.shape))
+
+
+def _add_rms_norm_partials(x: torch.Tensor, residual: "PartialSum", weight: torch.Tensor,
+                           eps: float, inplace: bool):
+    dev = nat.require_device(x, residual.parts, weight)
+    if tuple(residual.shape) != tuple(x.shape) or residual.dtype != x.dtype:
+        raise ValueError(f"partial sum {tuple(residual.shape)} {residual.dtype} does not match "
+                         f"x {tuple(x.shape)} {x.dtype}")
+    if weight.dim() != 1 or weight.shape[0] != x.shape[-1]:
+        raise ValueError(f"weight shape {tuple(weight.shape)} does not match hidden {x.shape[-1]}")
+    hidden = x.shape[-1]
+    x2 = x.reshape(-1, hidden)
+    if inplace and (x2.data_ptr() != x.data_ptr() or x2.stride(-1) != 1):
+        raise ValueError("inplace add_rms_norm needs x with unit stride over hidden")
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    if w.dtype != x.dtype and w.dtype != torch.float32:
+        w = w.to(x.dtype)
+    parts = residual.parts  # [S, rows, hidden] fp32, contiguous
+    y = torch.empty((x2.shape[0], hidden), dtype=x.dtype, device=dev)
+    s2 = x2 if inplace else torch.empty((x2.shape[0], hidden), dtype=x.dtype, device=dev)
+    lib = nat.load()
+    with _DeviceGuard(dev):
+        rc = lib.lc_add_rmsnorm_partials_fwd(
+            x2.data_ptr(), parts.data_ptr(), parts.shape[0], parts.stride(0), w.data_ptr(),
+            y.data_ptr(), s2.data_ptr(), x2.shape[0], hidden, x2.stride(0), parts.stride(1),
+            y.stride(0), s2.stride(0), float(eps), nat.lc_dtype(x), nat.lc_dtype(w), _stream(dev))
+    nat.check(rc, "lc_add_rmsnorm_partials_fwd")
     return y.view(x.shape), (x if inplace else s2.view(x.shape))
 
 
@@ -532,6 +568,66 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False,
             nat.lc_dtype(x), _stream(dev))
     nat.check(rc, "lc_decode_linear")
     return y
+
+
+class PartialSum:
+    """A projection's output left as fp32 split-K partials: the value is
+    round(0.0 + parts[0] + parts[1] + ...) in `dtype`, summed in that order
+    (what decode_linear itself writes). parts: [S, rows, N] fp32; `shape` is
+    the projection output's shape. add_rms_norm takes it as its residual and
+    forms the sum in its own pass; materialize() forms it on its own."""
+
+    def __init__(self, parts: torch.Tensor, shape, dtype: torch.dtype):
+        self.parts = parts
+        self.shape = torch.Size(shape)
+        self.dtype = dtype
+
+    @property
+    def device(self) -> torch.device:
+        return self.parts.device
+
+    def materialize(self) -> torch.Tensor:
+        acc = torch.zeros_like(self.parts[0])
+        for p in self.parts:
+            acc = acc + p
+        return acc.to(self.dtype).view(self.shape)
+
+
+def decode_linear_partials_applies(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """decode_linear_applies, plus N % 4 == 0 (the partials' float4 rows)."""
+    return decode_linear_applies(x, weight) and weight.shape[0] % 4 == 0
+
+
+def decode_linear_partials(x: torch.Tensor, weight: torch.Tensor, shares: int = 0) -> PartialSum:
+    """x @ weight.T (weight [N, K]) with the split-K sum left undone: a
+    PartialSum whose value equals decode_linear(x, weight). shares: K-shares
+    per row block of the weight (0 = the library's choice)."""
+    if _records_grad(x, weight):
+        raise RuntimeError("decode_linear_partials is inference-only (autograd is recording)")
+    if x.dtype != weight.dtype:
+        raise TypeError("x and weight must share a dtype")
+    if weight.dim() != 2 or x.shape[-1] != weight.shape[1]:
+        raise ValueError(f"x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match")
+    dev = nat.require_device(x, weight)
+    K = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    weight = weight if weight.stride(-1) == 1 else weight.contiguous()
+    M, N = x2.shape[0], weight.shape[0]
+    lib = nat.load()
+    S = int(shares) if shares > 0 else lib.lc_decode_linear_partial_count(N, K)
+    if S < 1:
+        raise ValueError(f"decode_linear_partials: unsupported sizes N={N} K={K}")
+    parts = torch.empty(S, M, N, dtype=torch.float32, device=dev)
+    if M:
+        with _DeviceGuard(dev):
+            rc = lib.lc_decode_linear_partials(
+                x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
+                parts.data_ptr(), M, N, K, S, nat.lc_dtype(x), _stream(dev))
+        nat.check(rc, "lc_decode_linear_partials")
+    return PartialSum(parts, (*lead, N), x.dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -113,7 +113,12 @@ class Llama3Attention(nn.Module):
         attention_mask: torch.Tensor | None = None,
         past_key_value: tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None = None,
         use_cache: bool = False,
+        partial_out: bool = False,
     ) -> tuple[torch.Tensor, tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None]:
+        """The reference's forward (attention.py:91-150). partial_out (an
+        extension, default off): at a decode step whose o_proj runs on the
+        native projection kernel, return its output as an `_ops.PartialSum`
+        (split-K partials) for `add_rms_norm` to add up."""
         bsz, seq_len, _ = x.shape
 
         if FusedLinearWeights.usable(self.q_proj, self.k_proj, self.v_proj):
@@ -156,6 +161,8 @@ class Llama3Attention(nn.Module):
                     attention_mask=attention_mask, uniform_length=cache.uniform_length)
             out = out.transpose(1, 2).reshape(bsz, seq_len, self.num_heads * self.head_dim)
             wo = self.o_proj.weight
+            if partial_out and _ops.decode_linear_partials_applies(out, wo):
+                return _ops.decode_linear_partials(out, wo), cache
             if _ops.decode_linear_applies(out, wo):
                 return _ops.decode_linear(out, wo), cache
             return self.o_proj(out), cache

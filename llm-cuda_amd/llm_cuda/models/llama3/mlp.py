@@ -28,13 +28,19 @@ class Llama3MLP(nn.Module):
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
         self._gate_up = FusedLinearWeights(self.gate_proj, self.up_proj)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, partial_out: bool = False) -> torch.Tensor:
+        """The reference's forward (mlp.py:39-43). partial_out (an extension,
+        default off): at a decode step whose down_proj runs on the native
+        projection kernel, return its output as an `_ops.PartialSum` (split-K
+        partials) for `add_rms_norm` to add up."""
         if FusedLinearWeights.usable(self.gate_proj, self.up_proj):
             n = self.gate_proj.weight.shape[0]
             w = self._gate_up.weight()
             if _ops.decode_linear_applies(x, w, swiglu=True):
                 h = _ops.decode_linear(x, w, swiglu=True)
                 wd = self.down_proj.weight
+                if partial_out and _ops.decode_linear_partials_applies(h, wd):
+                    return _ops.decode_linear_partials(h, wd)
                 if _ops.decode_linear_applies(h, wd):
                     return _ops.decode_linear(h, wd)
                 return self.down_proj(h)

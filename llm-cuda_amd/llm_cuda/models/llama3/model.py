@@ -50,6 +50,7 @@ class Llama3DecoderLayer(nn.Module):
         attention_mask: torch.Tensor | None = None,
         past_key_value: tuple[torch.Tensor, torch.Tensor] | PagedKVLayerCache | None = None,
         use_cache: bool = False,
+        partial_out: bool = False,
     ):
         """The layer with its last residual add left to the caller.
 
@@ -57,7 +58,10 @@ class Llama3DecoderLayer(nn.Module):
         mlp_out, present) with the layer's output = x_mid + mlp_out, so that a
         stack can fuse that add with the next layer's input norm. Each add is
         rounded to x's dtype and normalised exactly as the separate add and
-        norm of the reference layer (model.py:29-42).
+        norm of the reference layer (model.py:29-42). With partial_out, a
+        decode step's o_proj and down_proj outputs may be `_ops.PartialSum`s
+        (pending may be one too): their split-K sums are formed by the add +
+        norm that consumes them, with the same value.
         """
         norm_in = self.input_layernorm
         if pending is None:
@@ -65,10 +69,11 @@ class Llama3DecoderLayer(nn.Module):
         else:
             h, x = add_rms_norm(x, pending, norm_in.weight, norm_in.eps)
         attn_out, present = self.self_attn(
-            h, attention_mask=attention_mask, past_key_value=past_key_value, use_cache=use_cache)
+            h, attention_mask=attention_mask, past_key_value=past_key_value, use_cache=use_cache,
+            partial_out=partial_out)
         norm_post = self.post_attention_layernorm
         h, x = add_rms_norm(x, attn_out, norm_post.weight, norm_post.eps)
-        return x, self.mlp(h), present
+        return x, self.mlp(h, partial_out=partial_out), present
 
 
 class Llama3Model(nn.Module):
@@ -92,8 +97,9 @@ class Llama3Model(nn.Module):
         presents: list[tuple[torch.Tensor, torch.Tensor]] = []
         # Each layer's closing residual add is fused with the next norm (the
         # next layer's input norm, or the final norm): `pending` carries the
-        # MLP output still to be added to x.
-        pending: torch.Tensor | None = None
+        # MLP output still to be added to x (at a decode step, its split-K
+        # partials: the add + norm forms their sum).
+        pending = None
         for idx, layer in enumerate(self.layers):
             if paged:
                 layer_past = past_key_values.get_layer(idx)
@@ -101,7 +107,7 @@ class Llama3Model(nn.Module):
                 layer_past = None if past_key_values is None else past_key_values[idx]
             x, pending, present = layer.forward_split(
                 x, pending, attention_mask=attention_mask, past_key_value=layer_past,
-                use_cache=use_cache)
+                use_cache=use_cache, partial_out=True)
             if use_cache and not paged and present is not None:
                 presents.append(present)
         if pending is None:

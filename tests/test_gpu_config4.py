@@ -121,9 +121,14 @@ class _Capture:
 
     @staticmethod
     def _hook(ins, outs, tuple_out):
+        from llm_cuda.kernels._ops import PartialSum
+
         def fn(mod, args, out):
             ins.append(args[0].detach().clone())
-            outs.append((out[0] if tuple_out else out).detach().clone())
+            o = out[0] if tuple_out else out
+            # o_proj / down_proj outputs may be split-K partials whose sum the
+            # next add + norm forms: record that value
+            outs.append(o.materialize() if isinstance(o, PartialSum) else o.detach().clone())
         return fn
 
     def remove(self):

@@ -210,3 +210,45 @@ def test_c_abi_strided_output_and_errors():
                               stream)
     assert rc != 0
     assert b"workspace" in lib.lc_last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,shares", [
+    (32, 4096, 4096, 0), (32, 4096, 14336, 0), (32, 4096, 4096, 4), (9, 1000, 1280, 5),
+    (5, 256, 1152, 3), (1, 64, 128, 1), (32, 6144, 4096, 2), (3, 300, 2304, 9)])
+def test_partials_sum_equals_decode_linear(dtype, M, N, K, shares):
+    """lc_decode_linear_partials: the shares' fp32 partials, added to 0.0 in
+    share order and rounded, equal lc_decode_linear's output bit for bit at
+    the same share count (the same tiles per share and the same sum order), and
+    the oracle to one ulp. Covers both tile shapes (K % 256 == 0 and == 128)
+    and the library's share choice."""
+    from llm_cuda import _native as nat
+    from llm_cuda.kernels import _ops
+
+    x, w = _inputs(M, N, K, dtype, False, seed=M + 3 * N + K)
+    ps = _ops.decode_linear_partials(x, w, shares=shares)
+    S = ps.parts.shape[0]
+    if shares == 0:
+        assert S == nat.load().lc_decode_linear_partial_count(N, K)
+    assert ps.parts.shape == (S, M, N) and ps.shape == (M, N) and ps.dtype == dtype
+    y = ps.materialize()
+    assert torch.equal(y, _ops.decode_linear(x, w, splits=S))
+    _check(y, _ref(x, w, False), 1.0)
+
+
+def test_partials_arguments_rejected():
+    """Shares that do not divide a row block's tiles, N % 4 != 0, misaligned
+    partials: errors before any launch."""
+    from llm_cuda import _native as nat
+
+    lib = nat.load()
+    x, w = _inputs(4, 256, 1024, torch.bfloat16, False, seed=41)  # 64-row blocks of 4 tiles
+    parts = torch.empty(8, 4, 256, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for N, shares, off, what in ((256, 3, 0, b"divide"), (254, 1, 0, b"N=254"),
+                                 (256, 2, 4, b"aligned")):
+        rc = lib.lc_decode_linear_partials(x.data_ptr(), 1024, w.data_ptr(), 1024,
+                                           parts.data_ptr() + off, 4, N, 1024, shares,
+                                           nat.lc_dtype(x), stream)
+        assert rc != 0 and what in lib.lc_last_error(), lib.lc_last_error()
+    assert lib.lc_decode_linear_partial_count(256, 1000) == -1

@@ -186,3 +186,45 @@ def test_predicates_true_on_device(cuda):
     c = torch.randn(4, 64, device=cuda, dtype=torch.float16)
     assert can_use_triton_rope(x, c, c) is True
     assert can_use_triton_rope(x[..., :63], c[:, :63], c[:, :63]) is False
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,hidden", [(32, 4096), (7, 1004), (3, 32768), (5, 14336)])
+@pytest.mark.parametrize("n_parts", [1, 3, 4, 6])
+def test_add_rmsnorm_over_partial_sums(cuda, dtype, rows, hidden, n_parts):
+    """lc_add_rmsnorm_partials_fwd: the residual given as fp32 partials equals
+    lc_add_rmsnorm_fwd with residual = round(0.0 + p_0 + p_1 + ...) bit for bit
+    (y and the sum), over the row kernel's paths: vectors held in registers
+    (4096, 14336), unaligned rows (1004), the two-pass loop (32768), and more
+    than four partials (a second batch of loads)."""
+    from llm_cuda.kernels import _ops
+
+    g = torch.Generator(device=cuda).manual_seed(rows * 31 + hidden + n_parts)
+    x = torch.randn(rows, 1, hidden, generator=g, device=cuda).to(dtype)
+    parts = torch.randn(n_parts, rows, hidden, generator=g, device=cuda) * 0.5
+    w = (1.0 + 0.1 * torch.randn(hidden, generator=g, device=cuda)).to(dtype)
+    ps = _ops.PartialSum(parts, (rows, 1, hidden), dtype)
+    r = ps.materialize()
+    y, s = _ops.add_rms_norm(x, ps, w, 1e-5)
+    y_ref, s_ref = _ops.add_rms_norm(x, r, w, 1e-5)
+    assert torch.equal(s, s_ref) and torch.equal(y, y_ref)
+    # in place, and with an fp32 weight
+    x2 = x.clone()
+    y2, s2 = _ops.add_rms_norm(x2, ps, w.float(), 1e-5, inplace=True)
+    y2_ref, _ = _ops.add_rms_norm(x, r, w.float(), 1e-5)
+    assert s2.data_ptr() == x2.data_ptr() and torch.equal(x2, s_ref) and torch.equal(y2, y2_ref)
+
+
+def test_partial_sum_materialize_order(cuda):
+    """PartialSum's value: fp32 partials added to 0.0 in order, then rounded
+    (checked on values whose sum depends on the order)."""
+    from llm_cuda.kernels import _ops
+
+    big, tiny = 2.0 ** 24, 1.0
+    parts = torch.tensor([[[big]], [[tiny]], [[-big]]], device=cuda)
+    ps = _ops.PartialSum(parts, (1, 1), torch.float32)
+    assert ps.materialize().item() == 0.0  # (big + 1) rounds to big in fp32, then - big
+    rev = _ops.PartialSum(parts.flip(0), (1, 1), torch.float32)
+    assert rev.materialize().item() == 1.0  # -big + 1 is exact, then + big
+    mid = _ops.PartialSum(parts[[0, 2, 1]], (1, 1), torch.float32)
+    assert mid.materialize().item() == 1.0

@@ -154,6 +154,46 @@ def test_bf16_8b_layer_shape_paged_vs_full(cuda):
     assert (got - full[:, 66:]).abs().max().item() <= 3e-2 * max(1.0, scale)
 
 
+def test_decode_step_partial_sums_are_bit_exact(cuda, monkeypatch):
+    """At a bf16 decode step o_proj and down_proj leave their split-K sums to
+    the add + RMSNorm after them (fp32 partials): the step's hidden states and
+    logits equal, bit for bit, the same step with both projections summing in
+    their own kernel."""
+    from llm_cuda.kernels import _ops
+    from llm_cuda.models.llama3.kv_cache import PagedKVCache
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    cfg = _small_config(hidden_size=512, intermediate_size=1536, num_hidden_layers=3,
+                        num_attention_heads=8, num_key_value_heads=2, vocab_size=4096)
+    torch.manual_seed(3)
+    model = Llama3ForCausalLM(cfg).to(device=cuda, dtype=torch.bfloat16).eval()
+    B = 6
+    ids = torch.randint(0, cfg.vocab_size, (B, 40), device=cuda)
+    calls = {"partials": 0}
+    orig = _ops.decode_linear_partials
+
+    def counting(*a, **k):
+        calls["partials"] += 1
+        return orig(*a, **k)
+
+    monkeypatch.setattr(_ops, "decode_linear_partials", counting)
+
+    def run():
+        cache = PagedKVCache.create(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
+                                    64, 16, cuda, torch.bfloat16, batch_size=B)
+        with torch.no_grad():
+            model(input_ids=ids[:, :37], past_key_values=cache, use_cache=True)
+            return [model(input_ids=ids[:, i:i + 1], past_key_values=cache,
+                          use_cache=True)["logits"] for i in range(37, 40)]
+
+    deferred = run()
+    assert calls["partials"] == 3 * 2 * cfg.num_hidden_layers  # o and down, every layer, 3 steps
+    monkeypatch.setattr(_ops, "decode_linear_partials_applies", lambda x, w: False)
+    summed = run()
+    for a, b in zip(deferred, summed):
+        assert torch.equal(a, b)
+
+
 def test_fused_projections_match_separate(cuda):
     """Inference runs q/k/v and gate/up as one GEMM each against the concatenated
     weights; with autograd recording, the separate Linear calls run. Both give
