@@ -36,6 +36,10 @@
 // arrive, which sums the partials in workgroup order (the result does not
 // depend on which came last), runs the epilogue and returns the ticket counter
 // to zero. No second launch, and no workgroup waits for another.
+//
+// Partial output (lc_decode_linear_partials, mode 0): a grid of whole shares,
+// each writing its fp32 partial to [share][M][N] with no hand-off; the
+// consumer adds the shares (lc_add_rmsnorm_partials_fwd).
 #include <limits.h>
 #include <algorithm>
 #include <math.h>
@@ -49,8 +53,8 @@ namespace {
 
 using namespace lc_attn;
 
-// (Two-wave workgroups for mode 1 -- 448 row blocks of 32 columns, two per
-// CU, instead of 224 blocks on 256 CUs -- measured slower.)
+// Four waves, one workgroup per CU (the LDS ring takes 120-156 KiB). (Two-wave
+// workgroups, two per CU, measured slower in an earlier whole-block layout.)
 constexpr int kDlWaves = 4;
 constexpr int kDlBatch = 32;            // x rows per launch (the MFMA's N)
 constexpr int kDlTileElems = 16384;     // weight elements per tile: ROWS x columns
