@@ -185,7 +185,11 @@ def _add_rms_norm_partials(x: torch.Tensor, residual: "PartialSum", weight: torc
     w = weight if weight.is_contiguous() else weight.contiguous()
     if w.dtype != x.dtype and w.dtype != torch.float32:
         w = w.to(x.dtype)
-    parts = residual.parts  # [S, rows, hidden] fp32, contiguous
+    parts = residual.parts  # [S, rows, hidden] fp32, unit stride over hidden
+    if (parts.dtype != torch.float32 or parts.dim() != 3
+            or tuple(parts.shape[1:]) != (x2.shape[0], hidden) or parts.stride(2) != 1):
+        raise ValueError(f"partials must be fp32 [S, {x2.shape[0]}, {hidden}] with unit stride "
+                         f"over hidden; got {tuple(parts.shape)} strides {parts.stride()}")
     y = torch.empty((x2.shape[0], hidden), dtype=x.dtype, device=dev)
     s2 = x2 if inplace else torch.empty((x2.shape[0], hidden), dtype=x.dtype, device=dev)
     lib = nat.load()

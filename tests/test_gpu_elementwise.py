@@ -228,3 +228,20 @@ def test_partial_sum_materialize_order(cuda):
     assert rev.materialize().item() == 1.0  # -big + 1 is exact, then + big
     mid = _ops.PartialSum(parts[[0, 2, 1]], (1, 1), torch.float32)
     assert mid.materialize().item() == 1.0
+
+
+def test_add_rmsnorm_partials_layout_checked(cuda):
+    """Partials that are not [S, rows, hidden] fp32 with unit stride over
+    hidden are rejected before any launch."""
+    from llm_cuda.kernels import _ops
+
+    x = torch.randn(4, 256, device=cuda).bfloat16()
+    w = torch.ones(256, device=cuda).bfloat16()
+    good = torch.randn(2, 4, 256, device=cuda)
+    bad = [torch.randn(2, 256, 4, device=cuda).transpose(1, 2),  # strided over hidden
+           good.to(torch.float16),                                  # not fp32
+           torch.randn(2, 4, 128, device=cuda)]                     # wrong width
+    for parts in bad:
+        with pytest.raises((ValueError, TypeError)):
+            _ops.add_rms_norm(x, _ops.PartialSum(parts, (4, 256), x.dtype), w, 1e-5)
+    _ops.add_rms_norm(x, _ops.PartialSum(good, (4, 256), x.dtype), w, 1e-5)
