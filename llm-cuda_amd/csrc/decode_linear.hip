@@ -430,19 +430,6 @@ int64_t dl_grid(int64_t n_blocks, int64_t k_tiles, int requested, int n_cu) {
   return (U + per0 - 1) / per0;
 }
 
-int dl_n_cu() {
-  static int cached = 0;
-  if (cached == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      cached = n;
-    else
-      cached = 256;
-  }
-  return cached;
-}
-
 // Rows per block: 64 (512-byte runs per row) where K allows 256-column
 // tiles, else 128.
 int dl_rows(int64_t K) { return K % (2 * kDlKc) == 0 ? 64 : 128; }
@@ -473,7 +460,7 @@ bool dl_plan(int64_t N, int64_t K, int mode, int splits, DlPlan* p) {
   p->n_blocks = (N + out_cols - 1) / out_cols;
   if (p->n_blocks > kDlMaxBlocks) return false;
   p->k_tiles = K / (kDlTileElems / p->rows);
-  p->grid = dl_grid(p->n_blocks, p->k_tiles, splits, dl_n_cu());
+  p->grid = dl_grid(p->n_blocks, p->k_tiles, splits, lc_cu_count());
   const int64_t U = p->n_blocks * p->k_tiles;
   // No partials when every run is a whole number of whole blocks.
   const bool whole = U % p->grid == 0 && (U / p->grid) % p->k_tiles == 0;
@@ -577,7 +564,7 @@ int64_t lc_decode_linear_partial_count(int64_t N, int64_t K) {
   const int rows = dl_rows(K);
   const int64_t n_blocks = (N + rows - 1) / rows;
   if (n_blocks > kDlMaxBlocks) return -1;
-  return dl_shares(n_blocks, K / (kDlTileElems / rows), dl_n_cu());
+  return dl_shares(n_blocks, K / (kDlTileElems / rows), lc_cu_count());
 }
 
 int lc_decode_linear_partials(const void* x, int64_t x_row_stride, const void* weight,
@@ -605,7 +592,7 @@ int lc_decode_linear_partials(const void* x, int64_t x_row_stride, const void* w
   LC_REQUIRE(n_blocks <= kDlMaxBlocks, "lc_decode_linear_partials: N=%lld too large",
              (long long)N);
   const int64_t kt = K / (kDlTileElems / rows);
-  const int64_t s = shares > 0 ? shares : dl_shares(n_blocks, kt, dl_n_cu());
+  const int64_t s = shares > 0 ? shares : dl_shares(n_blocks, kt, lc_cu_count());
   LC_REQUIRE(kt % s == 0, "lc_decode_linear_partials: %lld shares do not divide the %lld tiles "
              "of a row block", (long long)s, (long long)kt);
   LC_REQUIRE(n_blocks * kt < (1LL << 31), "lc_decode_linear_partials: too many tiles");

@@ -25,6 +25,19 @@ int lc_check_launch(const char* what) {
   return LC_OK;
 }
 
+int lc_cu_count() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cached = n;
+    else
+      cached = 256;
+  }
+  return cached;
+}
+
 extern "C" {
 
 // Major * 10000 + minor * 100 + patch.

@@ -12,6 +12,8 @@
 int lc_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Checks hipGetLastError() after a launch; returns LC_OK or the hipError_t.
 int lc_check_launch(const char* what);
+// Compute units of the current device (queried once; 256 if the query fails).
+int lc_cu_count();
 
 #define LC_REQUIRE(cond, ...)                  \
   do {                                         \

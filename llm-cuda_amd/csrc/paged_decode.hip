@@ -455,6 +455,56 @@ struct StepArgs {
   int32_t* counters;  // [B]: zero on entry, zero again on return
 };
 
+// Longest-first order of the (sequence, split) pairs for a ragged batch of
+// B <= 64 sequences (lane i holds sequence i) and split_tokens <= 2^24 (the
+// select's keys are 31 bits): every whole split (split_tokens
+// tokens) first, sequence by sequence, then each sequence's final partial
+// split, longest first (ties: lower sequence first). The hardware deals
+// workgroups to the XCDs and, inside each, to its shader engines round-robin
+// by id, whatever each one's work; in this order consecutive ids carry equal
+// or similar work, so every engine gets an even share and its queue ends with
+// its shortest splits. Returns (b << 16) | split of pair r and the sequence's
+// length in len_out, or -1 when r is past the last pair.
+__device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane, int& len_out) {
+  const int li = lane < a.B ? seq_len_of(a, lane) : 0;
+  const int whole = li / a.split_tokens;
+  const int rem = li - whole * a.split_tokens;
+  int incl = whole;  // inclusive prefix sum of the whole splits
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += t;
+  }
+  const int n_whole = __builtin_amdgcn_readlane(incl, 63);
+  int bb, sp;
+  if (r < n_whole) {
+    bb = __builtin_ctzll(__ballot(incl > r));
+    sp = r - (__builtin_amdgcn_readlane(incl, bb) - __builtin_amdgcn_readlane(whole, bb));
+  } else {
+    // The k-th largest key (remainder, then lower lane first) by a radix
+    // select over the key bits, on ballots: the candidates shrink to one lane.
+    unsigned long long cand = __ballot(rem > 0);
+    int k = r - n_whole;
+    if (k >= __popcll(cand)) return -1;
+    const unsigned key = (static_cast<unsigned>(rem) << 6) | static_cast<unsigned>(63 - lane);
+    const int top = 31 - __builtin_clz((static_cast<unsigned>(a.split_tokens) << 6) | 63u);
+    for (int bit = top; bit >= 0; --bit) {
+      const unsigned long long ones = __ballot((key >> bit) & 1u) & cand;
+      const int c = __popcll(ones);
+      if (k < c) {
+        cand = ones;
+      } else {
+        k -= c;
+        cand &= ~ones;
+      }
+    }
+    bb = __builtin_ctzll(cand);
+    sp = __builtin_amdgcn_readlane(whole, bb);
+  }
+  len_out = __builtin_amdgcn_readlane(li, bb);
+  return (bb << 16) | sp;
+}
+
 // Single-split decode (max_splits == 1) for page_size % 32 == 0: one
 // workgroup of W waves per (b, kv head, group of <= 16 query heads). The
 // sequence's 32-token steps are dealt out evenly to the W waves by its
@@ -476,7 +526,12 @@ struct StepArgs {
 // seq_lens[b] = p + 1 and returns counters[b] to zero; every workgroup takes
 // its ticket after its last read of seq_lens[b]. Results equal the RoPE,
 // append and decode launches in sequence, up to fp32 summation order.
-template <typename T, int DPAD, bool HB, bool STEP, bool PRE>
+//
+// ORD (several splits, B <= 64, not STEP): a one-dimensional grid whose
+// workgroup i takes unit i % (Hkv * n_hgroups) of pair i / (Hkv * n_hgroups)
+// in the order of ordered_pair; the splits and their partials are the same
+// as in the (units, B, splits) grid.
+template <typename T, int DPAD, bool HB, bool STEP, bool PRE, bool ORD = false>
 __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_cluster_kernel(
     DecodeArgs a, T* __restrict__ out, int64_t o_sb, int64_t o_sh, float* __restrict__ lse_out,
     StepArgs sa) {
@@ -497,12 +552,25 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int kvh = blockIdx.x / a.n_hgroups;
-  const int hg = blockIdx.x - kvh * a.n_hgroups;
-  const int b = blockIdx.y;
+  int kvh, hg, b, split, ord_len = 0;
+  if constexpr (ORD) {
+    const int units = a.Hkv * a.n_hgroups;
+    const int r = blockIdx.x / units;
+    const int u = blockIdx.x - r * units;
+    const int pair = ordered_pair(a, r, lane, ord_len);
+    if (pair < 0) return;
+    kvh = u / a.n_hgroups;
+    hg = u - kvh * a.n_hgroups;
+    b = pair >> 16;
+    split = pair & 0xffff;
+  } else {
+    kvh = blockIdx.x / a.n_hgroups;
+    hg = blockIdx.x - kvh * a.n_hgroups;
+    b = blockIdx.y;
+    split = blockIdx.z;
+  }
   const int cap = a.max_pages * a.P;
   // This workgroup's split: tokens [s_begin, s_begin + split_tokens).
-  const int split = blockIdx.z;
   const int s_begin = split * a.split_tokens;
   // PRE (the split's pages fit 64 block-table entries): the window of the row
   // from the split's first page is loaded whole (one entry per lane) together
@@ -513,7 +581,7 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   if constexpr (PRE)
     row_entry = a.bt[(int64_t)b * a.bt_stride + min(window_base + lane, a.max_pages - 1)];
   const int p_new = STEP ? a.seq_lens[b] : 0;  // the new token's position
-  const int len = STEP ? min(max(p_new, 0), cap) : seq_len_of(a, b);
+  const int len = STEP ? min(max(p_new, 0), cap) : ORD ? ord_len : seq_len_of(a, b);
   if constexpr (PRE) {
     row_entry = window_base + lane < a.max_pages ? row_entry : -1;
     // Keep the row load here, beside the length's, rather than sunk to its use.
@@ -1031,7 +1099,25 @@ int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, f
   // (split_tokens - 1) / P + 2 pages; one split reads pages 0 .. max_pages-1.
   const bool pre = a.max_splits == 1 ? a.max_pages <= 64
                                      : (a.split_tokens - 1) / a.P + 2 <= 64;
-  if (a.bias != nullptr && pre)
+  // Longest-first order where the workgroups take more than one round of the
+  // CUs (with one round every workgroup starts at once and the order cannot
+  // matter, and computing it would only lengthen each one's start).
+  const int64_t n_wg = (int64_t)a.Hkv * a.n_hgroups * a.B * a.max_splits;
+  if (a.max_splits > 1 && a.B <= 64 && a.split_tokens <= (1 << 24) && n_wg > lc_cu_count()) {
+    const dim3 g1(static_cast<unsigned>(n_wg));
+    if (a.bias != nullptr && pre)
+      paged_decode_cluster_kernel<T, DPAD, true, false, true, true>
+          <<<g1, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
+    else if (a.bias != nullptr)
+      paged_decode_cluster_kernel<T, DPAD, true, false, false, true>
+          <<<g1, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
+    else if (pre)
+      paged_decode_cluster_kernel<T, DPAD, false, false, true, true>
+          <<<g1, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
+    else
+      paged_decode_cluster_kernel<T, DPAD, false, false, false, true>
+          <<<g1, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
+  } else if (a.bias != nullptr && pre)
     paged_decode_cluster_kernel<T, DPAD, true, false, true>
         <<<grid, threads, 0, st>>>(a, o, o_sb, o_sh, lse, none);
   else if (a.bias != nullptr)
