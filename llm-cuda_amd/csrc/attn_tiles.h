@@ -56,6 +56,19 @@ __device__ __forceinline__ void pf_barrier() {
 //    position bits.
 // A plain XOR with r mod 16 fails the second (4 rows map onto the same 4
 // positions); swapping the two 2-bit halves of r mod 16 satisfies both.
+// Position of the q-th workgroup of a (batch, kv head, head group) unit in
+// the causal kernels' heaviest-first row-group order, q < n: the order is
+// reversed inside every other run of four. Each XCD deals its workgroups to
+// its four shader engines round-robin, so with the plain order the first
+// engine took the heaviest row group of every four (at 128 row groups per
+// unit about 5% more work than the fourth); alternating the direction gives
+// the four engines equal sums. A final partial run stays a permutation of
+// itself.
+__device__ __forceinline__ int pf_snake(int q, int n) {
+  const int s = (q & ~3) | ((q & 4) ? 3 - (q & 3) : (q & 3));
+  return s < n ? s : q;
+}
+
 template <int CPR>
 __device__ __forceinline__ int pf_swz(int r) {
   if constexpr (CPR == 16) {

@@ -187,13 +187,15 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   // to the 8 XCDs (each with its own L2). Work item W = xcd * per_xcd + k is
   // given to the k-th workgroup landing on XCD xcd, so each XCD walks whole
   // (b, kv head, head group) units in turn and their K/V stays in its L2.
-  // Within a unit the heaviest (latest) row groups come first.
+  // Within a unit the heaviest (latest) row groups come first, reversed in
+  // every other run of four (pf_snake) so the XCD's shader engines get equal
+  // shares.
   const int nwg = gridDim.x;
   const int lin = blockIdx.x;
   int work = lin;
   if ((nwg & 7) == 0) work = (lin & 7) * (nwg >> 3) + (lin >> 3);
   const int unit = work / n_rbg;
-  const int rbg = n_rbg - 1 - (work - unit * n_rbg);
+  const int rbg = n_rbg - 1 - pf_snake(work - unit * n_rbg, n_rbg);
   const int kvh_hg = unit % (a.Hkv * n_hg);
   const int b = unit / (a.Hkv * n_hg);
   const int kvh = kvh_hg / n_hg;

@@ -447,7 +447,7 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
   int work = lin;
   if ((nwg & 7) == 0) work = (lin & 7) * (nwg >> 3) + (lin >> 3);
   const int unit = work / n_rbg;
-  const int rbg = n_rbg - 1 - (work - unit * n_rbg);
+  const int rbg = n_rbg - 1 - pf_snake(work - unit * n_rbg, n_rbg);
   const int kvh_hg = unit % (a.Hkv * n_hg);
   const int b = unit / (a.Hkv * n_hg);
   const int kvh = kvh_hg / n_hg;
