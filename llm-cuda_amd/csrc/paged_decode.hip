@@ -457,9 +457,9 @@ struct StepArgs {
 
 // Longest-first order of the (sequence, split) pairs for a ragged batch of
 // B <= 64 sequences (lane i holds sequence i) and split_tokens <= 2^24 (the
-// select's keys are 31 bits): every whole split (split_tokens
-// tokens) first, sequence by sequence, then each sequence's final partial
-// split, longest first (ties: lower sequence first). The hardware deals
+// select's keys are 31 bits): every whole split (split_tokens tokens) first,
+// sequence by sequence, then each sequence's final partial split, longest
+// first (ties: lower sequence first). The hardware deals
 // workgroups to the XCDs and, inside each, to its shader engines round-robin
 // by id, whatever each one's work; in this order consecutive ids carry equal
 // or similar work, so every engine gets an even share and its queue ends with
@@ -1103,7 +1103,8 @@ int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, f
   // CUs (with one round every workgroup starts at once and the order cannot
   // matter, and computing it would only lengthen each one's start).
   const int64_t n_wg = (int64_t)a.Hkv * a.n_hgroups * a.B * a.max_splits;
-  if (a.max_splits > 1 && a.B <= 64 && a.split_tokens <= (1 << 24) && n_wg > lc_cu_count()) {
+  if (a.max_splits > 1 && a.B <= 64 && a.split_tokens <= (1 << 24) && n_wg > lc_cu_count() &&
+      n_wg < (1LL << 31)) {
     const dim3 g1(static_cast<unsigned>(n_wg));
     if (a.bias != nullptr && pre)
       paged_decode_cluster_kernel<T, DPAD, true, false, true, true>
