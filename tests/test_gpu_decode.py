@@ -192,13 +192,14 @@ def test_baseline_70b_long_context_subset(cuda):
     assert_lse_close(lse, ref_lse)
 
 
-@pytest.mark.parametrize("dtype,P,split,masked", [
-    (torch.bfloat16, 64, 2048, False),   # config 2's kernel: table window loaded with the length
-    (torch.float16, 64, 3072, False),
-    (torch.bfloat16, 32, 2048, False),   # splits over 64 pages: per-wave table loads
-    (torch.bfloat16, 64, 2048, True),    # additive key mask
+@pytest.mark.parametrize("dtype,P,split,masked,B", [
+    (torch.bfloat16, 64, 2048, False, 64),   # config 2's kernel: table window loaded with the length
+    (torch.float16, 64, 3072, False, 64),
+    (torch.bfloat16, 32, 2048, False, 64),   # splits over 64 pages: per-wave table loads
+    (torch.bfloat16, 64, 2048, True, 64),    # additive key mask
+    (torch.bfloat16, 64, 3072, False, 37),   # lanes past the batch hold no sequence
 ])
-def test_longest_first_order_matches_split_major(cuda, dtype, P, split, masked):
+def test_longest_first_order_matches_split_major(cuda, dtype, P, split, masked, B):
     """A ragged batch of at most 64 sequences whose split workgroups take more
     than one round of the CUs runs its (sequence, split) pairs longest first:
     the whole splits, then each sequence's final partial split by decreasing
@@ -206,14 +207,17 @@ def test_longest_first_order_matches_split_major(cuda, dtype, P, split, masked):
     equals, bit for bit, the same sequences in a batch of 65 (which keeps the
     split-major grid), and matches the oracle. Lengths cover an empty
     sequence, one token, whole splits only (no partial split), equal
-    remainders in different sequences and the longest length."""
+    remainders in different sequences and the longest length; a batch of 37
+    leaves lanes of the ordering wave without a sequence."""
     from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
 
-    g = torch.Generator().manual_seed(P + split)
+    g = torch.Generator().manual_seed(P + split + B)
     lens = torch.randint(0, 6001, (64,), generator=g).tolist()
     lens[:8] = [0, 1, 31, split, 2 * split, split + 7, 2 * split + 7, 6000]
+    lens = lens[:B]
     Hq, Hkv, D = 32, 8, 128
-    q, kp, vp, bt, sl = _paged_case(lens + [100], Hq, Hkv, D, P, dtype, cuda, seed=P + 3)
+    q, kp, vp, bt, sl = _paged_case(lens + [100] * (65 - B), Hq, Hkv, D, P, dtype, cuda,
+                                    seed=P + 3)
     mask = None
     if masked:
         mask = torch.randn(65, 1, 1, 6000, generator=g)
@@ -227,12 +231,12 @@ def test_longest_first_order_matches_split_major(cuda, dtype, P, split, masked):
         return paged_decode_attention(q[:n].to(cuda), kp.to(cuda), vp.to(cuda), bt[:n].to(cuda),
                                       sl[:n].to(cuda), return_lse=True, attention_mask=m, **kw)
 
-    out64, lse64 = run(64)
+    out64, lse64 = run(B)
     out65, lse65 = run(65)
-    assert torch.equal(out64, out65[:64]), "longest-first order changed the output"
-    assert torch.equal(lse64, lse65[:64])
-    ref, ref_lse = paged_decode(q[:64], kp, vp, bt[:64], sl[:64],
-                                bias=None if mask is None else mask[:64, :, 0].float())
+    assert torch.equal(out64, out65[:B]), "longest-first order changed the output"
+    assert torch.equal(lse64, lse65[:B])
+    ref, ref_lse = paged_decode(q[:B], kp, vp, bt[:B], sl[:B],
+                                bias=None if mask is None else mask[:B, :, 0].float())
     assert_close(out64, ref, ATOL[dtype], f"longest-first P={P} split={split}")
     assert_lse_close(lse64, ref_lse)
 
