@@ -456,16 +456,105 @@ struct StepArgs {
 };
 
 // Longest-first order of the (sequence, split) pairs for a ragged batch of
-// B <= 64 sequences (lane i holds sequence i) and split_tokens <= 2^24 (the
-// select's keys are 31 bits): every whole split (split_tokens tokens) first,
-// sequence by sequence, then each sequence's final partial split, longest
-// first (ties: lower sequence first). The hardware deals
-// workgroups to the XCDs and, inside each, to its shader engines round-robin
-// by id, whatever each one's work; in this order consecutive ids carry equal
-// or similar work, so every engine gets an even share and its queue ends with
-// its shortest splits. Returns (b << 16) | split of pair r and the sequence's
-// length in len_out, or -1 when r is past the last pair.
-__device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane, int& len_out) {
+// B <= 64 * kOrdChunks sequences (lane i of chunk c holds sequence 64c + i)
+// and split_tokens <= 2^23 (the select's keys are 31 bits): every whole split
+// (split_tokens tokens) first, sequence by sequence, then each sequence's
+// final partial split, longest first (ties: lower sequence first). The
+// hardware deals workgroups to the XCDs and, inside each, to its shader
+// engines round-robin by id, whatever each one's work; in this order
+// consecutive ids carry equal or similar work, so every engine gets an even
+// share and its queue ends with its shortest splits. Returns (b << 16) |
+// split of pair r and the sequence's length in len_out, or -1 when r is past
+// the last pair.
+constexpr int kOrdChunks = 4;
+__device__ __forceinline__ int ordered_pair_chunked(const DecodeArgs& a, int r, int lane,
+                                                    int& len_out) {
+  const int nc = (a.B + 63) >> 6;  // chunks in use (uniform)
+  // Chunks past nc hold no sequence; every loop below skips them (uniform
+  // branches), so a batch of <= 64 pays for one chunk only.
+  int li[kOrdChunks] = {}, whole[kOrdChunks] = {}, rem[kOrdChunks] = {}, incl[kOrdChunks] = {};
+  int carry = 0;  // whole splits of the earlier chunks
+#pragma unroll
+  for (int c = 0; c < kOrdChunks; ++c) {
+    if (c >= nc) break;
+    const int bi = c * 64 + lane;
+    li[c] = bi < a.B ? seq_len_of(a, bi) : 0;
+    whole[c] = li[c] / a.split_tokens;
+    rem[c] = li[c] - whole[c] * a.split_tokens;
+    int x = whole[c];  // inclusive prefix sum of the whole splits
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(x, off, 64);
+      if (lane >= off) x += t;
+    }
+    incl[c] = x + carry;
+    carry = __builtin_amdgcn_readlane(incl[c], 63);
+  }
+  const int n_whole = carry;
+  int bb = -1, sp = 0, lb = 0;
+  if (r < n_whole) {
+#pragma unroll
+    for (int c = 0; c < kOrdChunks; ++c) {
+      if (c >= nc) break;
+      const unsigned long long m = __ballot(incl[c] > r);
+      if (bb < 0 && m != 0) {
+        const int l = __builtin_ctzll(m);
+        bb = c * 64 + l;
+        sp = r - (__builtin_amdgcn_readlane(incl[c], l) - __builtin_amdgcn_readlane(whole[c], l));
+        lb = __builtin_amdgcn_readlane(li[c], l);
+      }
+    }
+  } else {
+    // The k-th largest key (remainder, then lower sequence first) by a radix
+    // select over the key bits, on ballots: the candidates shrink to one lane.
+    unsigned long long cand[kOrdChunks] = {};
+    unsigned key[kOrdChunks] = {};
+    int k = r - n_whole, n_part = 0;
+#pragma unroll
+    for (int c = 0; c < kOrdChunks; ++c) {
+      if (c >= nc) break;
+      cand[c] = __ballot(rem[c] > 0);
+      n_part += __popcll(cand[c]);
+      key[c] = (static_cast<unsigned>(rem[c]) << 8) | static_cast<unsigned>(255 - (c * 64 + lane));
+    }
+    if (k >= n_part) return -1;
+    const int top = 31 - __builtin_clz((static_cast<unsigned>(a.split_tokens) << 8) | 255u);
+    for (int bit = top; bit >= 0; --bit) {
+      unsigned long long ones[kOrdChunks];
+      int cnt = 0;
+#pragma unroll
+      for (int c = 0; c < kOrdChunks; ++c) {
+        if (c >= nc) break;
+        ones[c] = __ballot((key[c] >> bit) & 1u) & cand[c];
+        cnt += __popcll(ones[c]);
+      }
+      const bool take = k < cnt;
+      if (!take) k -= cnt;
+#pragma unroll
+      for (int c = 0; c < kOrdChunks; ++c) {
+        if (c >= nc) break;
+        cand[c] = take ? ones[c] : (cand[c] & ~ones[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kOrdChunks; ++c) {
+      if (c >= nc) break;
+      if (bb < 0 && cand[c] != 0) {
+        const int l = __builtin_ctzll(cand[c]);
+        bb = c * 64 + l;
+        sp = __builtin_amdgcn_readlane(whole[c], l);
+        lb = __builtin_amdgcn_readlane(li[c], l);
+      }
+    }
+  }
+  len_out = lb;
+  return (bb << 16) | sp;
+}
+
+// The same order for B <= 64 (one sequence per lane): the batches this path
+// was first measured on take the shorter code (the chunked form measured ~1%
+// slower at 64 sequences).
+__device__ __forceinline__ int ordered_pair_64(const DecodeArgs& a, int r, int lane, int& len_out) {
   const int li = lane < a.B ? seq_len_of(a, lane) : 0;
   const int whole = li / a.split_tokens;
   const int rem = li - whole * a.split_tokens;
@@ -481,8 +570,6 @@ __device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane
     bb = __builtin_ctzll(__ballot(incl > r));
     sp = r - (__builtin_amdgcn_readlane(incl, bb) - __builtin_amdgcn_readlane(whole, bb));
   } else {
-    // The k-th largest key (remainder, then lower lane first) by a radix
-    // select over the key bits, on ballots: the candidates shrink to one lane.
     unsigned long long cand = __ballot(rem > 0);
     int k = r - n_whole;
     if (k >= __popcll(cand)) return -1;
@@ -503,6 +590,11 @@ __device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane
   }
   len_out = __builtin_amdgcn_readlane(li, bb);
   return (bb << 16) | sp;
+}
+
+__device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane, int& len_out) {
+  return a.B <= 64 ? ordered_pair_64(a, r, lane, len_out)
+                   : ordered_pair_chunked(a, r, lane, len_out);
 }
 
 // Single-split decode (max_splits == 1) for page_size % 32 == 0: one
@@ -527,7 +619,7 @@ __device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane
 // its ticket after its last read of seq_lens[b]. Results equal the RoPE,
 // append and decode launches in sequence, up to fp32 summation order.
 //
-// ORD (several splits, B <= 64, not STEP): a one-dimensional grid whose
+// ORD (several splits, B <= 256, not STEP): a one-dimensional grid whose
 // workgroup i takes unit i % (Hkv * n_hgroups) of pair i / (Hkv * n_hgroups)
 // in the order of ordered_pair; the splits and their partials are the same
 // as in the (units, B, splits) grid.
@@ -1103,7 +1195,8 @@ int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, f
   // CUs (with one round every workgroup starts at once and the order cannot
   // matter, and computing it would only lengthen each one's start).
   const int64_t n_wg = (int64_t)a.Hkv * a.n_hgroups * a.B * a.max_splits;
-  if (a.max_splits > 1 && a.B <= 64 && a.split_tokens <= (1 << 24) && n_wg > lc_cu_count() &&
+  if (a.max_splits > 1 && a.B <= 64 * kOrdChunks && a.split_tokens <= (1 << 23) &&
+      n_wg > lc_cu_count() &&
       n_wg < (1LL << 31)) {
     const dim3 g1(static_cast<unsigned>(n_wg));
     if (a.bias != nullptr && pre)

@@ -681,7 +681,7 @@ def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens
         length; s = 1 is one split over the capacity. Measured: config 4
         (256 units) 43.6 us against 46.0 us for 512-token splits; config 5
         (64 units x 4 splits of 8256) 168.9 us against 174.8 us at 2048.
-      * lengths unknown (ragged), >= n_cus units and at most 64 sequences
+      * lengths unknown (ragged), >= n_cus units and at most 256 sequences
         (the library then runs the splits longest first): s = 6 * n_cus /
         units splits per unit (rounded up), each a 1/s share of the capacity
         rounded up to 1024 tokens, at least 2048, more splits where a wave's
@@ -709,7 +709,7 @@ def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens
                     break
                 s += 1
             split = -(-(-(-length // s)) // 64) * 64
-        elif units >= n_cus and batch <= 64:
+        elif units >= n_cus and batch <= 256:
             s = -(-6 * n_cus // units)
             while True:
                 split = max(2048, -(-(-(-capacity_tokens // s)) // 1024) * 1024)

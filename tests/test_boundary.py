@@ -218,17 +218,17 @@ def test_split_heuristic():
     # workgroup splits per unit, 8000 / 3 rounded up to 3072 tokens
     assert choose_split_tokens(64, 8, 4, 8000) == 3072
     assert takes_workgroup_splits(512, 3072, 3, 64, 128, 8000)
-    # the same shape with 65 sequences (no longest-first order): 2048-token
-    # splits, about 8 per CU
-    assert choose_split_tokens(65, 8, 4, 8000) == 2048
+    # more than 256 sequences (no longest-first order): about 8 splits per CU,
+    # here one per unit (2056 units)
+    assert choose_split_tokens(257, 8, 4, 8000) == 8000
     # config 4 (32 sequences at 2049 tokens, 256 units): one split over the
     # capacity when the common length is known; when not, six splits per unit
-    # would be 352 tokens, so the 2048-token floor; 512-token one-wave splits
-    # for more than 64 sequences
+    # would be 352 tokens, so the 2048-token floor; over 256 sequences with
+    # fewer units than 8 rounds of the CUs, 512-token one-wave splits
     assert choose_split_tokens(32, 8, 4, 2112, 64, 128, 2049) == 2112
     assert choose_split_tokens(32, 8, 4, 2112) == 2048
-    assert choose_split_tokens(80, 8, 4, 2112) == 512
-    assert not takes_workgroup_splits(640, 512, 5, 64, 128, 2112)
+    assert choose_split_tokens(257, 1, 4, 2112) == 512
+    assert not takes_workgroup_splits(257, 512, 5, 64, 128, 2112)
     # long ragged contexts: more splits until a wave's share fits 64 pages
     # (100000 / 3 -> 34816 would give 68 pages per wave; 100000 / 4 -> 25600)
     assert choose_split_tokens(64, 8, 4, 100000) == 25600

@@ -198,29 +198,32 @@ def test_baseline_70b_long_context_subset(cuda):
     (torch.bfloat16, 32, 2048, False, 64),   # splits over 64 pages: per-wave table loads
     (torch.bfloat16, 64, 2048, True, 64),    # additive key mask
     (torch.bfloat16, 64, 3072, False, 37),   # lanes past the batch hold no sequence
+    (torch.bfloat16, 64, 3072, False, 150),  # three 64-lane chunks of sequences
 ])
 def test_longest_first_order_matches_split_major(cuda, dtype, P, split, masked, B):
-    """A ragged batch of at most 64 sequences whose split workgroups take more
+    """A ragged batch of at most 256 sequences whose split workgroups take more
     than one round of the CUs runs its (sequence, split) pairs longest first:
     the whole splits, then each sequence's final partial split by decreasing
     length. Every split is computed as in the split-major grid, so the output
-    equals, bit for bit, the same sequences in a batch of 65 (which keeps the
+    equals, bit for bit, the same sequences in a batch of 257 (which keeps the
     split-major grid), and matches the oracle. Lengths cover an empty
     sequence, one token, whole splits only (no partial split), equal
-    remainders in different sequences and the longest length; a batch of 37
-    leaves lanes of the ordering wave without a sequence."""
+    remainders in different sequences (also across 64-sequence chunks) and the
+    longest length; a batch of 37 leaves lanes of the ordering wave without a
+    sequence, one of 150 spans three chunks."""
     from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
 
     g = torch.Generator().manual_seed(P + split + B)
-    lens = torch.randint(0, 6001, (64,), generator=g).tolist()
+    lens = torch.randint(0, 6001, (B,), generator=g).tolist()
     lens[:8] = [0, 1, 31, split, 2 * split, split + 7, 2 * split + 7, 6000]
-    lens = lens[:B]
+    lens[-3:] = [lens[3] + 5, 2 * split + 7, 1]  # ties across the batch's chunks
+    n_ref = 257  # a batch this large keeps the split-major grid
     Hq, Hkv, D = 32, 8, 128
-    q, kp, vp, bt, sl = _paged_case(lens + [100] * (65 - B), Hq, Hkv, D, P, dtype, cuda,
+    q, kp, vp, bt, sl = _paged_case(lens + [100] * (n_ref - B), Hq, Hkv, D, P, dtype, cuda,
                                     seed=P + 3)
     mask = None
     if masked:
-        mask = torch.randn(65, 1, 1, 6000, generator=g)
+        mask = torch.randn(n_ref, 1, 1, 6000, generator=g)
         mask[9, ..., 500:900] = float("-inf")
         mask[10, ..., :3000] = -1e4
         mask = mask.to(dtype)
@@ -231,14 +234,14 @@ def test_longest_first_order_matches_split_major(cuda, dtype, P, split, masked, 
         return paged_decode_attention(q[:n].to(cuda), kp.to(cuda), vp.to(cuda), bt[:n].to(cuda),
                                       sl[:n].to(cuda), return_lse=True, attention_mask=m, **kw)
 
-    out64, lse64 = run(B)
-    out65, lse65 = run(65)
-    assert torch.equal(out64, out65[:B]), "longest-first order changed the output"
-    assert torch.equal(lse64, lse65[:B])
+    out_b, lse_b = run(B)
+    out_ref, lse_ref = run(n_ref)
+    assert torch.equal(out_b, out_ref[:B]), "longest-first order changed the output"
+    assert torch.equal(lse_b, lse_ref[:B])
     ref, ref_lse = paged_decode(q[:B], kp, vp, bt[:B], sl[:B],
                                 bias=None if mask is None else mask[:B, :, 0].float())
-    assert_close(out64, ref, ATOL[dtype], f"longest-first P={P} split={split}")
-    assert_lse_close(lse64, ref_lse)
+    assert_close(out_b, ref, ATOL[dtype], f"longest-first P={P} split={split} B={B}")
+    assert_lse_close(lse_b, ref_lse)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
