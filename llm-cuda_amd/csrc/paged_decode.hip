@@ -466,6 +466,20 @@ struct StepArgs {
 // share and its queue ends with its shortest splits. Returns (b << 16) |
 // split of pair r and the sequence's length in len_out, or -1 when r is past
 // the last pair.
+// Inclusive prefix sum over the wave's 64 lanes on DPP moves (no LDS round
+// trips): shifts of 1, 2, 4 and 8 lanes inside each 16-lane row, then the
+// row totals broadcast from lane 15 into rows 1 and 3 and from lane 31 into
+// rows 2 and 3. Lanes whose source lies outside the row read 0.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+
 constexpr int kOrdChunks = 4;
 __device__ __forceinline__ int ordered_pair_chunked(const DecodeArgs& a, int r, int lane,
                                                     int& len_out) {
@@ -481,13 +495,7 @@ __device__ __forceinline__ int ordered_pair_chunked(const DecodeArgs& a, int r, 
     li[c] = bi < a.B ? seq_len_of(a, bi) : 0;
     whole[c] = li[c] / a.split_tokens;
     rem[c] = li[c] - whole[c] * a.split_tokens;
-    int x = whole[c];  // inclusive prefix sum of the whole splits
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(x, off, 64);
-      if (lane >= off) x += t;
-    }
-    incl[c] = x + carry;
+    incl[c] = wave_incl_scan(whole[c]) + carry;  // prefix sum of the whole splits
     carry = __builtin_amdgcn_readlane(incl[c], 63);
   }
   const int n_whole = carry;
@@ -558,12 +566,7 @@ __device__ __forceinline__ int ordered_pair_64(const DecodeArgs& a, int r, int l
   const int li = lane < a.B ? seq_len_of(a, lane) : 0;
   const int whole = li / a.split_tokens;
   const int rem = li - whole * a.split_tokens;
-  int incl = whole;  // inclusive prefix sum of the whole splits
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += t;
-  }
+  const int incl = wave_incl_scan(whole);  // inclusive prefix sum of the whole splits
   const int n_whole = __builtin_amdgcn_readlane(incl, 63);
   int bb, sp;
   if (r < n_whole) {
