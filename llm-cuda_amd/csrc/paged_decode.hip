@@ -407,7 +407,11 @@ __global__ __launch_bounds__(64) void paged_decode_rows_kernel(DecodeArgs a) {
   const int split = blockIdx.z;
   const int kvh = blockIdx.x / a.n_hgroups;
   const int hg = blockIdx.x - kvh * a.n_hgroups;
-  const int b = blockIdx.y;
+  // Sequence b's split z sits at grid row (b - z) mod B: the hardware deals
+  // workgroups to each XCD's shader engines round-robin by id, so with b on
+  // the row every split of a sequence went to one engine; rotated, a
+  // sequence's splits spread over all four.
+  const int b = (blockIdx.y + blockIdx.z) % a.B;
   const int len = seq_len_of(a, b);
   const int t_begin = split * a.split_tokens;
   if (t_begin >= len) return;
@@ -948,7 +952,11 @@ paged_decode_lanes_kernel(DecodeArgs a) {
   const int split = blockIdx.z;
   const int kvh = blockIdx.x / a.n_hgroups;
   const int hg = blockIdx.x - kvh * a.n_hgroups;
-  const int b = blockIdx.y;
+  // Sequence b's split z sits at grid row (b - z) mod B: the hardware deals
+  // workgroups to each XCD's shader engines round-robin by id, so with b on
+  // the row every split of a sequence went to one engine; rotated, a
+  // sequence's splits spread over all four.
+  const int b = (blockIdx.y + blockIdx.z) % a.B;
   const int len = seq_len_of(a, b);
   const int t_begin = split * a.split_tokens;
   if (t_begin >= len) return;
