@@ -11,16 +11,18 @@ TFLOP/s), prefill_bwd (the attention backward at the config-3 shape), lm_head
 (fused lm_head + greedy argmax at the config-4 vocab), decode_linear (one
 decoder layer's decode-step projections on lc_decode_linear at the config-4
 shape),
-model8b (config 4, tok/s of a full 8B decode step), rmsnorm /
-swiglu / rope (bandwidth shapes of the fused elementwise kernels), copycal
-(counter calibration copy).
+model8b (config 4, tok/s of a full 8B decode step; --model-projections torch,
+the config as stated, or native), rmsnorm / swiglu / rope (bandwidth shapes
+of the fused elementwise kernels), copycal (counter calibration copy).
 
 Prints one JSON line with the driver's fields plus `roofline` (the dominant
 kernel against MI355X peaks) and `cpu_baseline` (the CPU oracle on the host
 cores, bounded sample). The default run also measures the other BASELINE
-configs, prefill TFLOP/s (config 3), the 8B decode step's tok/s (config 4) and
-long-context decode GB/s (config 5), each with its own roofline and CPU
-baseline, under `secondary` (`--no-secondary` skips them).
+configs, prefill TFLOP/s (config 3), long-context decode GB/s (config 5) and
+the 8B decode step's tok/s (config 4, with torch and with native
+projections), plus the elementwise evidence shapes and lm_head + argmax,
+each with its own roofline and CPU baseline, under `secondary`
+(`--no-secondary` skips them).
 """
 from __future__ import annotations
 
@@ -372,13 +374,16 @@ def run_lm_head(args):
         from oracle.lm_head import lm_head_argmax
 
         torch.set_num_threads(cpu_threads())
-        hs, ws = hidden.cpu(), weights[0].cpu()
-        secs = timed_cpu(lambda: lm_head_argmax(hs, ws), budget_s=40.0)
+        # a bounded sample: 1/8 of the vocabulary rows, the time scaled x8
+        vs = V // 8
+        hs, ws = hidden.cpu(), weights[0][:vs].cpu()
+        secs = timed_cpu(lambda: lm_head_argmax(hs, ws), budget_s=20.0) * (V / vs)
         result["cpu_baseline"] = {
             "value": round(nbytes / secs / 1e9, 3), "unit": "GB/s",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"the whole step (32 rows x vocab {V}), oracle.lm_head.lm_head_argmax "
-                      f"(fp64 dot products, rounded to bf16, first-index argmax): {secs:.3f} s"}
+            "sample": f"32 rows x vocab rows 0-{vs - 1} (1/8 of {V}), oracle.lm_head."
+                      f"lm_head_argmax (fp64 dot products, rounded to bf16, first-index "
+                      f"argmax), scaled x8: {secs:.3f} s per step"}
     return result
 
 
@@ -482,7 +487,7 @@ def _model8b_config():
                         max_position_embeddings=8192)
 
 
-def run_model(args):
+def run_model(args, projections=None, cpu_cache=None):
     """Benchmark config 4: one decode step of random-init Llama-3-8B (bf16), batch 32,
     paged KV at context 2048 (seeded random page permutation, pools ~N(0,1)).
 
@@ -490,12 +495,27 @@ def run_model(args):
     decode / o_proj / SwiGLU MLP, final norm, fused lm_head + greedy argmax) is
     captured once in a HIP graph; the graph starts by resetting every layer's
     seq_lens to 2048, so each replay decodes position 2048 against the same
-    cache. The first replay is checked against the eager step.
+    cache. Three replays, with eager work between them, are checked against
+    the eager step.
+
+    projections: "torch" (BASELINE config 4 as stated: the q/k/v, o, gate/up
+    and down projections are torch matmuls, hipBLASLt) or "native" (the same
+    step with lc_decode_linear for them); default --model-projections.
+    cpu_cache: a dict that keeps the CPU baseline between calls (it does not
+    depend on the projection path).
     """
+    import contextlib
+
     import torch
 
+    from llm_cuda.kernels import _ops
     from llm_cuda.models.llama3.kv_cache import PagedKVCache
     from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    projections = projections or args.model_projections
+    if projections not in ("torch", "native"):
+        raise ValueError(f"projections must be 'torch' or 'native', got {projections!r}")
+    proj_ctx = _ops.torch_projections() if projections == "torch" else contextlib.nullcontext()
 
     dev = torch.device("cuda", 0)
     cfg = _model8b_config()
@@ -526,7 +546,7 @@ def run_model(args):
         nxt, _, best = model.greedy_next_token(ids, cache, return_logit=True)
         return nxt, best
 
-    with torch.no_grad():
+    with torch.no_grad(), proj_ctx:
         reset()
         eager_ids, eager_logits = step()
         eager_logits = eager_logits.float().clone()
@@ -543,12 +563,15 @@ def run_model(args):
         reset()
         with torch.cuda.graph(graph):
             g_ids, g_logits = step()
-        reset()
-        graph.replay()
-        torch.cuda.synchronize()
-        diff = (g_logits.float() - eager_logits).abs().max().item()
-        if not torch.equal(g_ids, eager_ids) or diff > 1e-2:
-            raise RuntimeError(f"graph replay differs from eager step (max |dlogit| {diff})")
+        for rep in range(3):
+            reset()
+            graph.replay()
+            torch.cuda.synchronize()
+            diff = (g_logits.float() - eager_logits).abs().max().item()
+            if not torch.equal(g_ids, eager_ids) or diff > 1e-2:
+                raise RuntimeError(f"graph replay {rep} differs from eager step "
+                                   f"(max |dlogit| {diff})")
+            torch.zeros(1 << 20, device=dev).sum().item()  # eager work between replays
         # The fused lm_head + argmax picks the argmax of the full logits.
         reset()
         full = model(input_ids=ids, past_key_values=cache, use_cache=True)["logits"][:, -1, :]
@@ -562,8 +585,18 @@ def run_model(args):
     weights = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
     kv = cfg.num_hidden_layers * B * ctx * cfg.num_key_value_heads * cfg.head_dim * 2 * 2
     gbs = (weights + kv) / (ms * 1e-3) / 1e9
-    log(f"model8b: {ms:.3f} ms/step -> {tok_s:.0f} tok/s; weights {weights / 1e9:.2f} GB + KV "
-        f"{kv / 1e9:.2f} GB per step -> {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+    log(f"model8b ({projections} projections): {ms:.3f} ms/step -> {tok_s:.0f} tok/s; weights "
+        f"{weights / 1e9:.2f} GB + KV {kv / 1e9:.2f} GB per step -> {gbs:.0f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+    if projections == "torch":
+        proj_desc = ("torch F.linear (hipBLASLt), as BASELINE config 4 states: one GEMM for "
+                     "q/k/v and one for gate/up (concatenated weights), o and down; SwiGLU, "
+                     "RoPE + KV append + decode attention, add + RMSNorm and lm_head + argmax "
+                     "on the HIP kernels")
+        profile = "model8b_decode_step_torch_proj"
+    else:
+        proj_desc = "native lc_decode_linear: fused q/k/v, o, gate/up + SwiGLU, down"
+        profile = "model8b_decode_step"
     result = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tok/s", "ms_per_step": round(ms, 5),
         "dtype": "bf16",
@@ -571,15 +604,19 @@ def run_model(args):
                    "batch": B, "context": ctx, "page_size": P, "layers": cfg.num_hidden_layers,
                    "hidden": cfg.hidden_size, "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size,
                    "hip_graph": True, "bytes_per_step": weights + kv,
-                   "projections": "native lc_decode_linear: fused q/k/v, o, gate/up + "
-                                  "SwiGLU, down"},
+                   "projections": proj_desc},
         "roofline": {"bound": "hbm", "kernel": "whole decode step (weights + KV read once)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("model8b_decode_step")},
+                     "traffic": measured_traffic(profile)},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = _model_cpu_baseline(model, cfg, B, ctx)
+        if cpu_cache is not None and "model8b" in cpu_cache:
+            result["cpu_baseline"] = cpu_cache["model8b"]
+        else:
+            result["cpu_baseline"] = _model_cpu_baseline(model, cfg, B, ctx)
+            if cpu_cache is not None:
+                cpu_cache["model8b"] = result["cpu_baseline"]
     return result
 
 
@@ -697,19 +734,24 @@ def run_elementwise(args, kind: str):
         from oracle import elementwise as ref
 
         torch.set_num_threads(cpu_threads())
+        # bounded samples (a fraction of the rows, the time scaled up), so the
+        # default bench run stays short
         if kind == "rmsnorm":
-            xc, wc = xs[0].float().cpu(), w.float().cpu()
-            secs = timed_cpu(lambda: ref.rms_norm(xc, wc, 1e-5))
-            sample = "the full x (fp32 upcast), oracle.elementwise.rms_norm"
+            xc, wc = xs[0][:2048].float().cpu(), w.float().cpu()
+            secs = timed_cpu(lambda: ref.rms_norm(xc, wc, 1e-5), budget_s=4.0) * 8
+            sample = "rows 0-2047 of x (fp32 upcast), oracle.elementwise.rms_norm, scaled x8"
         elif kind == "swiglu":
-            gc, uc = gs[0][:4096].float().cpu(), us[0][:4096].float().cpu()
-            secs = timed_cpu(lambda: ref.swiglu(gc, uc)) * (gs[0].shape[0] / 4096)
-            sample = "rows 0-4095 of g, u (fp32 upcast), oracle.elementwise.swiglu, scaled x4"
+            gc, uc = gs[0][:1024].float().cpu(), us[0][:1024].float().cpu()
+            secs = timed_cpu(lambda: ref.swiglu(gc, uc), budget_s=4.0) * (gs[0].shape[0] / 1024)
+            sample = "rows 0-1023 of g, u (fp32 upcast), oracle.elementwise.swiglu, scaled x16"
         else:
-            qc, kc = pairs[0][0].float().cpu(), pairs[0][1].float().cpu()
+            qc = pairs[0][0][:1, :8].float().cpu()
+            kc = pairs[0][1][:1, :2].float().cpu()
             cc, sc = cos.float().cpu(), sin.float().cpu()
-            secs = timed_cpu(lambda: (ref.apply_rope(qc, cc, sc), ref.apply_rope(kc, cc, sc)))
-            sample = "the full Q and K (fp32 upcast), oracle.elementwise.apply_rope"
+            secs = timed_cpu(lambda: (ref.apply_rope(qc, cc, sc), ref.apply_rope(kc, cc, sc)),
+                             budget_s=4.0) * 16
+            sample = ("batch 0, q heads 0-7 and kv heads 0-1 (1/16 of Q and K, fp32 upcast), "
+                      "oracle.elementwise.apply_rope, scaled x16")
         cpu_gbs = nbytes / secs / 1e9
         log(f"cpu oracle: {secs:.3f} s -> {cpu_gbs:.2f} GB/s ({torch.get_num_threads()} threads)")
         result["cpu_baseline"] = {"value": round(cpu_gbs, 3), "unit": "GB/s",
@@ -778,12 +820,15 @@ def main() -> int:
                                  "lm_head", "decode_linear", "copycal",
                                  "rmsnorm", "swiglu", "rope"])
     parser.add_argument("--split-tokens", type=int, default=None)
+    parser.add_argument("--model-projections", choices=["torch", "native"], default="torch",
+                        help="model8b: projections as torch matmuls (BASELINE config 4 as "
+                             "stated) or on the native lc_decode_linear kernel")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--prefill-shape", default=None, metavar="B,Hq,Hkv,S,D",
                         help="prefill: another shape instead of config 3 (4,32,8,4096,128)")
     parser.add_argument("--no-secondary", dest="secondary", action="store_false",
-                        help="decode8b: skip the config 3, 4 and 5 figures added to the line "
-                             "under 'secondary'")
+                        help="decode8b: skip the figures of the other configs and kernels "
+                             "added to the line under 'secondary'")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
@@ -839,8 +884,11 @@ def main() -> int:
 def run_secondary(args) -> dict:
     """The BASELINE configs other than the headline one, measured in the same run
     after it with the same steps and warm-up: prefill attention TFLOP/s at
-    config 3, the full 8B decode step's tok/s at config 4 and long-context paged
-    decode GB/s at config 5. Each entry carries its own `roofline` (with the
+    config 3, long-context paged decode GB/s at config 5, the full 8B decode
+    step's tok/s at config 4 (with torch matmul projections as the config
+    states, and again with the native projection kernel), and the HBM figures
+    of the elementwise evidence shapes (RMSNorm, SwiGLU, RoPE) and of the fused
+    lm_head + argmax. Each entry carries its own `roofline` (with the
     counter-measured traffic of its profiles/ summary) and, unless
     --no-cpu-baseline, its bounded `cpu_baseline`. A failure is recorded, not
     raised, so the primary line is still printed."""
@@ -851,6 +899,7 @@ def run_secondary(args) -> dict:
 
     sub = copy.copy(args)
     sub.prefill_shape = None  # the secondary prefill figure is config 3
+    cpu_cache: dict = {}
     out = {}
     # Config 5 runs before the model step: right after the step's run the
     # decode measured ~2% slower (170.7 against 167.1 us on one box, back to
@@ -858,7 +907,12 @@ def run_secondary(args) -> dict:
     # step's own figure is the same in either order (4.955 / 4.956 ms).
     jobs = (("prefill_config3", run_prefill),
             ("decode70b_config5", lambda a: run_decode(a, decode70b_shape())),
-            ("decode_step_config4", run_model))
+            ("decode_step_config4", lambda a: run_model(a, "torch", cpu_cache)),
+            ("decode_step_config4_native_proj", lambda a: run_model(a, "native", cpu_cache)),
+            ("rmsnorm", lambda a: run_elementwise(a, "rmsnorm")),
+            ("swiglu", lambda a: run_elementwise(a, "swiglu")),
+            ("rope", lambda a: run_elementwise(a, "rope")),
+            ("lm_head", run_lm_head))
     for key, fn in jobs:
         try:
             r = fn(sub)

@@ -280,6 +280,13 @@ __global__ __launch_bounds__(64 * kDlWaves) void decode_linear_kernel(DlArgs a) 
       }
       const int g_first = dl_owner(blk_lo, U, G);
       const int g_last = dl_owner(blk_lo + kt - 1, U, G);
+      // Hand-off invariant (the ticket itself is relaxed): every partial store
+      // above is sc1 (agent-coherent, written through to L2) and has been
+      // acknowledged (the s_waitcnt) by every wave (the barrier) before the
+      // ticket is taken; the last workgroup's loads of the partials are sc1
+      // too and control-dependent on s_last, so they cannot be served from a
+      // stale L1 line or issued before the ticket. Dropping the wait, or a
+      // partial store without sc1, breaks the hand-off.
       __builtin_amdgcn_s_waitcnt(dl_waitcnt(0, 0));
       __syncthreads();
       if (tid == 0) {

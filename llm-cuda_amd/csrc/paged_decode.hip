@@ -1208,7 +1208,7 @@ int launch_cluster(const DecodeArgs& a, void* out, int64_t o_sb, int64_t o_sh, f
   const int64_t n_wg = (int64_t)a.Hkv * a.n_hgroups * a.B * a.max_splits;
   if (a.max_splits > 1 && a.B <= 64 * kOrdChunks && a.split_tokens <= (1 << 23) &&
       n_wg > lc_cu_count() &&
-      n_wg < (1LL << 31)) {
+      n_wg * threads < (1LL << 32)) {  // a 1-D dispatch's work-items fit 32 bits
     const dim3 g1(static_cast<unsigned>(n_wg));
     if (a.bias != nullptr && pre)
       paged_decode_cluster_kernel<T, DPAD, true, false, true, true>

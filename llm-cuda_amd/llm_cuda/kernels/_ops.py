@@ -7,6 +7,7 @@ device tensors; anything else raises (there is no second implementation).
 """
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
@@ -494,26 +495,53 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
 # models/llama3/attention.py:100-102,154 and mlp.py:35-43 at a decode step)
 # ---------------------------------------------------------------------------
 DECODE_LINEAR_MAX_ROWS = 32
+_NATIVE_PROJECTIONS = [True]
 _DL_COUNTERS: dict = {}
+# Counter buffers replaced by a larger one stay referenced here: a HIP graph
+# captured earlier may still hold their addresses.
+_DL_RETIRED: list = []
 
 
 def _decode_linear_counters(dev: torch.device, n: int) -> torch.Tensor:
-    """Zeroed int32 ticket counters for lc_decode_linear (each call returns its
-    counters to zero, so one buffer per device serves every call on a stream)."""
-    key = (dev.type, dev.index)
+    """Zeroed int32 ticket counters for lc_decode_linear, one buffer per
+    (device, stream): each call returns its counters to zero, so calls that
+    follow one another on a stream share the buffer, while calls on different
+    streams (which may overlap) never do."""
+    key = (dev.type, dev.index, _stream(dev))
     buf = _DL_COUNTERS.get(key)
     if buf is None or buf.numel() < n:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("decode_linear: run one call outside graph capture first "
                                "(its ticket counters are allocated and zeroed eagerly)")
+        if buf is not None:
+            _DL_RETIRED.append(buf)
         buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
         _DL_COUNTERS[key] = buf
     return buf
 
 
+@contextlib.contextmanager
+def torch_projections():
+    """Within the block, the model's decode-step projections run as torch
+    matmuls (F.linear, hipBLASLt on ROCm) instead of lc_decode_linear: every
+    decode_linear_applies answers False. This is the reference's own
+    projection path (nn.Linear, models/llama3/attention.py:100-102,154 and
+    mlp.py:39-43); the attention, RoPE, KV append, RMSNorm and SwiGLU kernels
+    are the same either way. Not thread-safe: it flips a module-wide switch."""
+    prev = _NATIVE_PROJECTIONS[0]
+    _NATIVE_PROJECTIONS[0] = False
+    try:
+        yield
+    finally:
+        _NATIVE_PROJECTIONS[0] = prev
+
+
 def decode_linear_applies(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False) -> bool:
     """True where decode_linear takes the call: bf16/f16 on the GPU, 1-32 rows,
-    K % 128 == 0, aligned rows, no autograd graph being recorded."""
+    K % 128 == 0, an output width N % 4 == 0, aligned rows, no autograd graph
+    being recorded, and not inside torch_projections()."""
+    if not _NATIVE_PROJECTIONS[0]:
+        return False
     if not (x.is_cuda and weight.is_cuda and x.dtype == weight.dtype
             and x.dtype in (torch.bfloat16, torch.float16) and weight.dim() == 2):
         return False
@@ -522,6 +550,9 @@ def decode_linear_applies(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = 
     if not (1 <= rows <= DECODE_LINEAR_MAX_ROWS and K % 128 == 0 and weight.shape[1] == K):
         return False
     if swiglu and weight.shape[0] % 2:
+        return False
+    # lc_decode_linear writes y rows of N elements with 8-byte stores
+    if (weight.shape[0] // 2 if swiglu else weight.shape[0]) % 4:
         return False
     if _records_grad(x, weight):
         return False
@@ -577,7 +608,7 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False,
 class PartialSum:
     """A projection's output left as fp32 split-K partials: the value is
     round(0.0 + parts[0] + parts[1] + ...) in `dtype`, summed in that order
-    (what decode_linear itself writes). parts: [S, rows, N] fp32; `shape` is
+    (what decode_linear itself writes when its split is the same). parts: [S, rows, N] fp32; `shape` is
     the projection output's shape. add_rms_norm takes it as its residual and
     forms the sum in its own pass; materialize() forms it on its own."""
 
@@ -604,8 +635,12 @@ def decode_linear_partials_applies(x: torch.Tensor, weight: torch.Tensor) -> boo
 
 def decode_linear_partials(x: torch.Tensor, weight: torch.Tensor, shares: int = 0) -> PartialSum:
     """x @ weight.T (weight [N, K]) with the split-K sum left undone: a
-    PartialSum whose value equals decode_linear(x, weight). shares: K-shares
-    per row block of the weight (0 = the library's choice)."""
+    PartialSum whose value equals decode_linear(x, weight) up to the order of
+    the fp32 split-K sums. It is bit-identical where lc_decode_linear's default
+    grid deals each row block out in equal whole K-shares (the library's
+    default `shares` is then that same split); elsewhere the K split, and so
+    the summation order, differs. shares: K-shares per row block of the
+    weight (0 = the library's choice)."""
     if _records_grad(x, weight):
         raise RuntimeError("decode_linear_partials is inference-only (autograd is recording)")
     if x.dtype != weight.dtype:

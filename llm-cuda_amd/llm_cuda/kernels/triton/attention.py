@@ -67,6 +67,21 @@ def _should_use_cuda_sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return False
 
 
+def _cuda_sdpa_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Causal attention of q, k, v [B, H, S, D] with scale 1/sqrt(D) and no mask
+    (reference: attention.py:61-69, which calls torch SDPA with is_causal=True).
+
+    Kept under the reference's name for callers that import or patch it; here
+    it runs the same gfx950 MFMA kernel as triton_fused_causal_attention (GQA
+    k/v with fewer heads are taken as well), so no second attention path
+    exists. Forward only, like the rest of the dispatcher's non-autograd path.
+    """
+    if not _gqa_compatible(q, k, v):
+        raise ValueError("q, k, v must be [batch, heads, seq, head_dim] with n_heads a "
+                         "multiple of n_kv_heads")
+    return _ops.prefill_attention(q, k, v)
+
+
 def _gqa_compatible(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or k.shape != v.shape:
         return False

@@ -273,6 +273,7 @@ def test_reference_attention_selectors_are_importable():
     from llm_cuda.kernels.triton.attention import (
         _select_attention_block_sizes,
         _select_attention_num_warps,
+        _cuda_sdpa_causal_attention,
         _should_use_cuda_sdpa,
         can_use_triton_fused_attention,
     )
@@ -288,6 +289,10 @@ def test_reference_attention_selectors_are_importable():
     q = torch.randn(1, 2, 1024, 64, dtype=torch.float16)
     assert _should_use_cuda_sdpa(q, q, q, attention_mask=None) is False
     assert can_use_triton_fused_attention(q[:, :, :8, :32], q[:, :, :8, :32], q[:, :, :8, :32]) is False
+    # the reference's SDPA helper keeps its name but runs the HIP kernel: on host
+    # tensors it raises rather than computing anything on the CPU
+    with pytest.raises((RuntimeError, ValueError)):
+        _cuda_sdpa_causal_attention(q, q, q)
 
 
 def test_empty_extents_accept_null_pointers():

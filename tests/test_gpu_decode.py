@@ -105,7 +105,7 @@ def test_paged_ragged_random_permutation(cuda, dtype, P):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("P", [16, 48])
 @pytest.mark.parametrize("D", [64, 48])
-def test_paged_lanes_kernel_small_head_dim(cuda, dtype, P, D):
+def test_paged_lanes_kernel_small_head_dim_g4(cuda, dtype, P, D):
     """Page sizes that are not multiples of 32 take the per-lane-page kernel;
     head_dim <= 64 runs its 64-wide instance (a tighter register budget)."""
     lens = [1, 17, 64, 100, 333, 48]

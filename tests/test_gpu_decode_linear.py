@@ -131,8 +131,36 @@ def test_consecutive_calls_reuse_workspace_and_counters():
         y = _ops.decode_linear(x, w, splits=8)
         _check(y, _ref(x, w, False), 1.0)
     torch.cuda.synchronize()
-    counters = _ops._DL_COUNTERS[("cuda", torch.cuda.current_device())]
+    dev = torch.device("cuda", torch.cuda.current_device())
+    counters = _ops._DL_COUNTERS[("cuda", dev.index, _ops._stream(dev))]
     assert int(counters.abs().sum()) == 0
+
+
+def test_counters_are_per_stream_and_odd_widths_route_elsewhere():
+    """Calls on two streams (which may overlap) get separate ticket counters;
+    an output width that is not a multiple of 4 is not taken (the library
+    stores y rows 8 bytes at a time), so callers fall back to F.linear."""
+    from llm_cuda.kernels import _ops
+
+    x, w = _inputs(4, 512, 512, torch.bfloat16, False, seed=21)
+    side = torch.cuda.Stream()
+    y0 = _ops.decode_linear(x, w)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        y1 = _ops.decode_linear(x, w)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    main = _ops._DL_COUNTERS[("cuda", dev.index, _ops._stream(dev))]
+    other = _ops._DL_COUNTERS[("cuda", dev.index, side.cuda_stream)]
+    assert main.data_ptr() != other.data_ptr()
+    assert _ops.decode_linear_applies(x, w)
+    assert not _ops.decode_linear_applies(x, w[:510])  # N = 510
+    xo, wo = _inputs(4, 1001, 512, torch.bfloat16, False, seed=22)
+    assert not _ops.decode_linear_applies(xo, wo)
+    xs, ws = _inputs(4, 1001, 512, torch.bfloat16, True, seed=23)
+    assert not _ops.decode_linear_applies(xs, ws, swiglu=True)
 
 
 def test_deterministic_per_split_count():

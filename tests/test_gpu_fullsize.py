@@ -49,6 +49,34 @@ def test_decode_config2_all_sequences(cuda):
     assert_lse_close(lse, ref_lse)
 
 
+def test_decode_config5_all_sequences(cuda):
+    """Config 5 exactly as bench.py times it: 8 sequences of 32768 tokens at the
+    70B attention shape (64/8 heads, D 128, P 64), block table
+    randperm(4096).view(8, 512), the library's default split (4 workgroup
+    splits of 8192 tokens per (sequence, kv head)), every output against the
+    oracle."""
+    from llm_cuda.kernels import _ops
+    from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
+
+    B, Hq, Hkv, D, P, L = 8, 64, 8, 128, 64, 32768
+    npg = L // P
+    g = torch.Generator().manual_seed(0)
+    bt = torch.randperm(B * npg, generator=g).to(torch.int32).view(B, npg)
+    gd = torch.Generator(device=cuda).manual_seed(0)
+    kp = torch.randn(B * npg, Hkv, P, D, generator=gd, device=cuda, dtype=torch.bfloat16)
+    vp = torch.randn(B * npg, Hkv, P, D, generator=gd, device=cuda, dtype=torch.bfloat16)
+    q = torch.randn(B, Hq, 1, D, generator=gd, device=cuda, dtype=torch.bfloat16)
+    sl = torch.full((B,), L, dtype=torch.int32)
+    # the split bench.py's config-5 call takes (nothing passed but the tensors)
+    split = _ops.choose_split_tokens(B, Hkv, Hq // Hkv, npg * P, P, D, None,
+                                     _ops._cu_count(cuda))
+    assert split == 8192
+    out, lse = paged_decode_attention(q, kp, vp, bt.to(cuda), sl.to(cuda), return_lse=True)
+    ref, ref_lse = paged_decode(q.cpu(), kp.cpu(), vp.cpu(), bt, sl)
+    assert_close(out.view(ref.shape), ref, ATOL[torch.bfloat16], "decode config 5")
+    assert_lse_close(lse, ref_lse)
+
+
 def _config3(device):
     from llm_cuda.models.llama3.rotary import apply_rotary, build_rope_cache
 

@@ -89,6 +89,17 @@ def test_reference_extension_entry(cuda):
     assert cuda_causal_attention_extension(q, k[:, :1], v[:, :1]) is None
 
 
+def test_reference_sdpa_helper_runs_the_hip_kernel(cuda):
+    """_cuda_sdpa_causal_attention (reference attention.py:61-69) keeps its name
+    and contract (causal, scale 1/sqrt(D), no mask) and runs the MFMA kernel."""
+    from llm_cuda.kernels.triton.attention import _cuda_sdpa_causal_attention
+
+    q, k, v = _qkv(2, 4, 4, 200, 200, 64, torch.bfloat16, cuda, seed=12)
+    out = _cuda_sdpa_causal_attention(q, k, v)
+    ref, _ = causal_attention(q.cpu(), k.cpu(), v.cpu())
+    assert_close(out, ref, ATOL[torch.bfloat16], "sdpa helper")
+
+
 def test_baseline_prefill_shape_head_subset(cuda):
     """Benchmark config 3: S 4096, D 128, RoPE theta 500000 by the HIP RoPE kernel,
     GQA 4:1; batch 1 and 2 kv-head groups (8 q heads) keep the oracle in seconds."""

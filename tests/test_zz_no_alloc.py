@@ -87,14 +87,30 @@ def test_noalloc_matches_workspace_entry_twice(cuda, second):
 
 
 def test_noalloc_rejects_partials_beyond_the_scratch(cuda):
-    """64 x 64 heads x 512 splits x head_dim 128 needs 1 GiB of partials: refused
-    with LC_EWORKSPACE before anything is launched (the pointers are never read)."""
+    """64 sequences x 64 heads x 512 splits x head_dim 128 needs 1 GiB of
+    partials: refused with LC_EWORKSPACE before anything is launched. Every
+    argument is a real device buffer of the shape it claims (empty sequences
+    over a one-page pool), so the call stays in bounds even if the size check
+    ever ran after a launch."""
     from llm_cuda import _native
 
     lib = _native.load()
-    assert lib.lc_paged_decode_workspace_bytes(64, 64, 128, 512) > 32 << 20
+    B, Hq, Hkv, D, P, max_pages, split, max_splits = 64, 64, 8, 128, 64, 512, 64, 512
+    assert lib.lc_paged_decode_workspace_bytes(B, Hq, D, max_splits) > 32 << 20
+    q = torch.zeros(B, Hq, D, dtype=torch.bfloat16, device=cuda)
+    kp = torch.zeros(1, Hkv, P, D, dtype=torch.bfloat16, device=cuda)
+    vp = torch.zeros_like(kp)
+    bt = torch.zeros(B, max_pages, dtype=torch.int32, device=cuda)
+    sl = torch.zeros(B, dtype=torch.int32, device=cuda)
+    out = torch.zeros(B, Hq, D, dtype=torch.bfloat16, device=cuda)
+    lse = torch.zeros(B, Hq, dtype=torch.float32, device=cuda)
     rc = lib.lc_paged_decode_fwd_noalloc(
-        16, 128, 128, 16, 16, 1, 1, 1, 16, 512, 512, 1 << 20, 16, 16, 128, 128, None, None, 0, 0,
-        0, 0, 64, 64, 8, 128, 64, 64, 512, 1.0, 2, None)
+        q.data_ptr(), q.stride(0), q.stride(1), kp.data_ptr(), vp.data_ptr(), kp.stride(0),
+        kp.stride(1), kp.stride(2), bt.data_ptr(), bt.stride(0), max_pages, kp.shape[0],
+        sl.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr(), None, 0, 0,
+        0, 0, B, Hq, Hkv, D, P, split, max_splits, 1.0, _native.lc_dtype(q),
+        torch.cuda.current_stream().cuda_stream)
     assert rc == LC_EWORKSPACE
     assert b"scratch" in lib.lc_last_error()
+    torch.cuda.synchronize()
+    assert not out.any() and not lse.any(), "a rejected call wrote its outputs"
