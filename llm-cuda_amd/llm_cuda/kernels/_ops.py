@@ -503,20 +503,27 @@ _DL_RETIRED: list = []
 
 
 def _decode_linear_counters(dev: torch.device, n: int) -> torch.Tensor:
-    """Zeroed int32 ticket counters for lc_decode_linear, one buffer per
-    (device, stream): each call returns its counters to zero, so calls that
-    follow one another on a stream share the buffer, while calls on different
-    streams (which may overlap) never do."""
-    key = (dev.type, dev.index, _stream(dev))
-    buf = _DL_COUNTERS.get(key)
-    if buf is None or buf.numel() < n:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("decode_linear: run one call outside graph capture first "
-                               "(its ticket counters are allocated and zeroed eagerly)")
-        if buf is not None:
-            _DL_RETIRED.append(buf)
-        buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
-        _DL_COUNTERS[key] = buf
+    """Zeroed int32 ticket counters for lc_decode_linear. Each call returns its
+    counters to zero, so calls that follow one another on a stream can share a
+    buffer; calls on different streams (which may overlap) must not. Eager
+    calls get one buffer per (device, stream). Calls captured into HIP graphs
+    share one more buffer per device (a capture cannot allocate and zero it:
+    every eager call makes sure it exists), so replays of graphs holding
+    decode_linear calls must not overlap on one device."""
+    capturing = torch.cuda.is_current_stream_capturing()
+    keys = [(dev.type, dev.index, "graphs")]
+    if not capturing:
+        keys.append((dev.type, dev.index, _stream(dev)))
+    for key in keys:
+        buf = _DL_COUNTERS.get(key)
+        if buf is None or buf.numel() < n:
+            if capturing:
+                raise RuntimeError("decode_linear: run one call outside graph capture first "
+                                   "(its ticket counters are allocated and zeroed eagerly)")
+            if buf is not None:
+                _DL_RETIRED.append(buf)
+            buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
+            _DL_COUNTERS[key] = buf
     return buf
 
 
