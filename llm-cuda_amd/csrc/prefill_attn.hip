@@ -139,6 +139,12 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 //   part B: P(t) V(t) (MFMA) with SM1(t+1) (VALU),
 // so the matrix cores and the VALU of one wave work side by side. A rescale
 // of O (rare: the running max grew by more than 2^8) is applied after part B.
+// Without a bias, only the first tile takes a row max: later tiles shift by
+// the reference max as it stands, and a check between part A and part B
+// (every lane's tile sum <= 2^8, which holds whenever every p <= 2^8) sends
+// the rare tiles that fail it through a fix-up that takes their row max from
+// the exponents and rescales before their PV. The max tree and its ballot
+// leave the loop (about a fifth of its non-exp VALU work).
 // LDS holds two K and two V tile buffers as separate arrays. Iteration t reads
 // K(t+1), V(t) and fetches K(t+2), V(t+1) by buffer-to-LDS DMA into the other
 // two; one barrier per iteration publishes them. Reads and DMA targets are
@@ -297,6 +303,7 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   v8 pop[2][2];     // P^T operands of the current tile (SM2 output)
   float alpha = 1.f;
   bool rescale = false;
+  float l_tile = 0.f;  // this lane's share of the current tile's row sum
   const int n_tiles = (kv_end + kPfKeys - 1) / kPfKeys;
 
   auto kbuf = [&](auto p_c) __attribute__((always_inline)) -> LC_LDS char* {
@@ -405,6 +412,69 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
     }
   };
 
+  // Without a bias, tiles after the first skip the row max: SM1L shifts by
+  // the current reference max, SM2L exponentiates and sums, and check_fix
+  // catches every tile where some p exceeds 2^8 (its lane's tile sum then
+  // does too): that tile's row max is taken from its exponents, and rows
+  // whose max is above the threshold move their reference max there (O and
+  // l rescaled, the tile's p recomputed) before the tile's PV.
+  auto sm1l = [&](int k0, auto mask_c) __attribute__((always_inline)) {
+    if constexpr (decltype(mask_c)::value) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+          if (key > qi + a.q_offset || key >= a.Skv) snx[kt][r] = -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xcu[kt][r] = fmaf(snx[kt][r], a.scale_log2, -m_ref);
+  };
+  auto sm2l = [&]() __attribute__((always_inline)) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = lc_exp2(xcu[kt][r]);
+        if (kt == 0) s0 += p; else s1 += p;
+        pop[kt][r >> 3][r & 7] = static_cast<T>(p);
+      }
+    l_tile = s0 + s1;
+  };
+  auto check_fix = [&]() __attribute__((always_inline)) {
+    if (__builtin_expect(__ballot(l_tile > 256.f) != 0, 0)) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, xcu[kt][r]);
+      mx = pf_half_max(mx);
+      const float d = mx > kPfRescaleLog2 ? mx : 0.f;
+      const float al = lc_exp2(-d);
+      m_ref += d;
+      l_lane *= al;
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= al;
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = lc_exp2(xcu[kt][r] - d);
+          if (kt == 0) s0 += p; else s1 += p;
+          pop[kt][r >> 3][r & 7] = static_cast<T>(p);
+        }
+      l_tile = s0 + s1;
+    }
+    l_lane += l_tile;
+  };
+
   // Iteration t (PAR = t & 1): reads K(t+1) from K buffer PAR ^ 1 and V(t)
   // from V buffer PAR; fetches K(t+2) -> K buffer PAR, V(t+1) -> V buffer
   // PAR ^ 1. MASK: tile t+1 needs the causal / key-range mask.
@@ -420,6 +490,40 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
       pf_dma_tile<NIW, RPI, ROW_B>(vbase, vbytes, vbuf(other), wave_s, voff, (t + 1) * vstep_b);
     const int k1 = (t + 1) * kPfKeys;
     const bool cur = live(t), nxt = live(t + 1);
+    if constexpr (BIAS == 0) {
+      if (cur && nxt) {
+        constexpr int NQ = 2 * KS, NP = 4 * DTL, LA = 4;
+        qk(kbuf(other));
+        sm2l();
+        __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (j + LA < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+        check_fix();
+        pv(vbuf(par_c));
+        sm1l(k1, mask_c);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * LA, 0);
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (j + LA < NP) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
+      } else {
+        if (nxt) qk(kbuf(other));
+        if (cur) {
+          sm2l();
+          check_fix();
+          pv(vbuf(par_c));
+        }
+        if (nxt) sm1l(k1, mask_c);
+      }
+      pf_barrier<true>();
+      return;
+    }
     if (cur && nxt) {
       qk(kbuf(other));
       sm2();
