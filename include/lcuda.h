@@ -177,6 +177,10 @@ LC_API int lc_prefill_attn_bwd(const void* q, const void* k, const void* v, cons
 /* Bytes of workspace lc_lm_head_argmax needs (per-block partial maxima). */
 LC_API int64_t lc_lm_head_argmax_workspace_bytes(int64_t B, int64_t V);
 
+/* int32 elements of the counters buffer lc_lm_head_argmax takes (packed
+ * per-row best keys and a ticket; 272 bytes). */
+LC_API int64_t lc_lm_head_argmax_counter_count(void);
+
 /* Greedy next token fused with the lm_head projection:
  *   ids[b] = argmax_v round(hidden[b, :] . weight[v, :])
  * round() = the fp32 dot product rounded to `dtype` (the dtype of the logits
@@ -187,11 +191,18 @@ LC_API int64_t lc_lm_head_argmax_workspace_bytes(int64_t B, int64_t V);
  * by model.py:214 (torch.argmax(logits[:, -1, :], dim=-1)) at the last position.
  * hidden: [B, K] with row stride hidden_row_stride; weight: [V, K] (nn.Linear
  * layout) with row stride weight_row_stride; ids: int64 [B].
- * bf16/f16 with K % 128 == 0 run on MFMA; other cases on a generic kernel. */
+ * bf16/f16 with K % 128 == 0 run on MFMA; other cases on a generic kernel.
+ * counters (may be NULL): an 8-byte aligned int32 buffer of
+ * lc_lm_head_argmax_counter_count() elements that is zero at entry and is
+ * left zero; with it the MFMA path selects the ids in its own launch
+ * (64-bit atomic max on packed (value, index) keys, the last workgroup
+ * writing the ids), without it a second launch reduces per-workgroup
+ * partials held in the workspace. Calls sharing one counters buffer must not
+ * overlap. */
 LC_API int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight,
                       int64_t weight_row_stride, int64_t B, int64_t K, int64_t V, int64_t* ids,
-                      float* max_logit, void* workspace, int64_t workspace_bytes, int dtype,
-                      void* stream);
+                      float* max_logit, void* workspace, int64_t workspace_bytes,
+                      int32_t* counters, int dtype, void* stream);
 
 /* Bytes of fp32 workspace lc_decode_linear needs for a given shape, mode and
  * split request (two partials per workgroup; 256 when every workgroup's share

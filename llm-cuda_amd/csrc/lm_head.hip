@@ -9,15 +9,21 @@
 //
 // Kernels:
 //   * lm_head_argmax_mfma_kernel (bf16/f16, K % 128 == 0, up to 32 hidden rows
-//     per launch): a workgroup owns 64 vocab rows and streams their weight rows
-//     through LDS in 256-column tiles (buffer-to-LDS DMA, 512-byte runs per
-//     row, a three-stage ring with two tiles in flight), together with the
-//     matching 256 columns of the hidden rows. Its 4 waves are 2 row groups x
+//     per launch): one workgroup per CU, each owning a contiguous range of
+//     vocab rows (V / grid, balanced to one row), which it walks in blocks of
+//     64 rows. Weight rows stream through LDS in 256-column tiles (buffer-to-
+//     LDS DMA, 512-byte runs per row, a three-stage ring with two tiles in
+//     flight) together with the matching 256 columns of the hidden rows; the
+//     ring runs on across block boundaries, so a block's start and finish
+//     overlap the neighbouring blocks' streams. Its 4 waves are 2 row groups x
 //     2 column halves; each computes
 //     logits^T[32 vocab x 32 batch] += W[32 x 16] hidden^T[16 x 32] on
-//     v_mfma_f32_32x32x16 over its half, the halves are added through LDS, and
-//     the epilogue rounds, takes each batch row's best (value, index) over the
-//     workgroup's 64 rows and writes it as a partial.
+//     v_mfma_f32_32x32x16 over its half; at a block's end the halves are
+//     added through LDS, rounded, and folded into each lane's running best
+//     (value, index). At the end the workgroup's best per batch row is either
+//     merged into packed 64-bit (value, index) keys with atomic max, the last
+//     workgroup (ticket) writing the ids and returning keys and ticket to zero
+//     (with a counters buffer), or written as a partial for the reduce kernel.
 //   * lm_head_argmax_generic_kernel (any dtype / K): one lane per vocab row.
 //   * lm_head_argmax_reduce_kernel: one workgroup per batch row reduces the
 //     partials to the final id (int64) and, optionally, the winning logit.
@@ -86,9 +92,40 @@ struct LhArgs {
   const void* weight;
   float* part_val;  // [n_wg][pstride]
   int* part_idx;
+  // Packed best keys [kLhBatch] followed by the ticket (zero at entry, left
+  // zero), or null: partials for the reduce kernel.
+  unsigned long long* keys;
+  int64_t* ids;
+  float* max_out;
   int64_t hs, ws;  // row strides (elements)
   int B, K, V, pstride;
 };
+
+// (value, index) as one unsigned 64-bit key whose order is lh_better's: the
+// high word orders the values (NaN above +inf, -0 taken as +0), the low word
+// is ~index, so among equal values the smaller index is larger. Key 0 is
+// below every (value, index) pair.
+__device__ __forceinline__ unsigned long long lh_pack(float x, int idx) {
+  // x + 0 turns -0 into +0 (round to nearest) and keeps every other value;
+  // negative values flip every bit, others only the sign bit. Branch-free.
+  const uint32_t b = __float_as_uint(x + 0.f);
+  const uint32_t m = static_cast<uint32_t>(static_cast<int32_t>(b) >> 31);
+  const uint32_t hi = x != x ? 0xFFFFFFFFu : (b ^ (m | 0x80000000u));
+  return (static_cast<unsigned long long>(hi) << 32) | static_cast<uint32_t>(~idx);
+}
+__device__ __forceinline__ unsigned long long lh_max_key(unsigned long long a,
+                                                         unsigned long long b) {
+  return a > b ? a : b;
+}
+__device__ __forceinline__ float lh_unpack_value(unsigned long long key) {
+  const uint32_t hi = static_cast<uint32_t>(key >> 32);
+  if (hi == 0xFFFFFFFFu) return __uint_as_float(0x7FC00000u);
+  return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
+}
+__device__ __forceinline__ int lh_unpack_index(unsigned long long key) {
+  return static_cast<int>(~static_cast<uint32_t>(key));
+}
+constexpr int kLhCounterInts = (kLhBatch * 8 + 16) / 4;  // keys + ticket (+ padding)
 
 template <typename T>
 __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhArgs a) {
@@ -102,14 +139,15 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   constexpr int NIW_H = kLhBatch / (RPI * kLhWaves);
   constexpr int W_B = kLhRows * ROW_B;
   constexpr int H_B = kLhBatch * ROW_B;
-  __shared__ __align__(16) char w0[W_B];
-  __shared__ __align__(16) char w1[W_B];
-  __shared__ __align__(16) char w2[W_B];
-  __shared__ __align__(16) char h0[H_B];
-  __shared__ __align__(16) char h1[H_B];
-  __shared__ __align__(16) char h2[H_B];
-  __shared__ float red_v[kLhRowWaves][32];
-  __shared__ int red_i[kLhRowWaves][32];
+  constexpr int XCH = kLhRowWaves * 16 * 64;      // floats per half-sum exchange buffer
+  // Three-stage rings for the weight and hidden tiles, addressed by a
+  // run-time stage (the DMA is issued as untracked assembly, so the compiler
+  // does not order LDS reads after it: the loop's waits and barriers do).
+  __shared__ __align__(16) char wring[kLhStages][W_B];
+  __shared__ __align__(16) char hring[kLhStages][H_B];
+  // Two exchange buffers (block parity) for the column halves' sums; the
+  // final per-workgroup reduction reuses the one the last block left free.
+  __shared__ __align__(16) float xch[2][XCH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -119,12 +157,16 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   const int hh = lane >> 5;
   const int rw = wave_s % kLhRowWaves;  // row group
   const int kh = wave_s / kLhRowWaves;  // column half of each tile
-  const int v0 = blockIdx.x * kLhRows;
-  const int rows_valid = min(kLhRows, a.V - v0);
-  const T* wbase = static_cast<const T*>(a.weight) + (int64_t)v0 * a.ws;
-  // Rows past the vocabulary (and hidden rows past B) are out of the
-  // descriptors' range and land in LDS as zeros.
-  const int wbytes = static_cast<int>(((int64_t)(rows_valid - 1) * a.ws + a.K) * sizeof(T));
+  // This workgroup's vocab rows [r_begin, r_end), in blocks of kLhRows.
+  const int nwg = gridDim.x;
+  const int r_begin = static_cast<int>((int64_t)a.V * blockIdx.x / nwg);
+  const int r_end = static_cast<int>((int64_t)a.V * (blockIdx.x + 1) / nwg);
+  const int nb = (r_end - r_begin + kLhRows - 1) / kLhRows;
+  const int n_tiles = (a.K + kLhKc - 1) / kLhKc;
+  const int G = nb * n_tiles;  // tiles of the whole range
+  const T* wbase = static_cast<const T*>(a.weight);
+  // Rows past the range (and hidden rows past B) are out of the descriptors'
+  // range and land in LDS as zeros.
   const int hbytes = static_cast<int>(((int64_t)(a.B - 1) * a.hs + a.K) * sizeof(T));
   const PfLoadOffsets<NIW_W> woff = [&] {
     PfLoadOffsets<NIW_W> o;
@@ -158,23 +200,15 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
     raddr[s] = l32 * ROW_B + (((kh * (CPR / 2) + hh * (CPR / 4) + s) ^ lh_swz(l32)) << 4);
   const int wrow0 = rw * 32 * ROW_B;
 
-  auto wbuf = [&](auto st_c) __attribute__((always_inline)) -> LC_LDS char* {
-    constexpr int S = decltype(st_c)::value;
-    if constexpr (S == 0) return (LC_LDS char*)w0;
-    else if constexpr (S == 1) return (LC_LDS char*)w1;
-    else return (LC_LDS char*)w2;
-  };
-  auto hbuf = [&](auto st_c) __attribute__((always_inline)) -> LC_LDS char* {
-    constexpr int S = decltype(st_c)::value;
-    if constexpr (S == 0) return (LC_LDS char*)h0;
-    else if constexpr (S == 1) return (LC_LDS char*)h1;
-    else return (LC_LDS char*)h2;
-  };
-  auto fetch = [&](int t, auto st_c) __attribute__((always_inline)) {
-    pf_dma_tile_untracked<NIW_W, RPI, ROW_B, kLhWeightNt>(wbase, wbytes, wbuf(st_c), wave_s, woff,
-                                                   t * ROW_B);
-    pf_dma_tile_untracked<NIW_H, RPI, ROW_B, false>(a.hidden, hbytes, hbuf(st_c), wave_s, hoff,
-                                                    t * ROW_B);
+  // Tile ft of block fb into ring stage st.
+  auto fetch = [&](int fb, int ft, int st) __attribute__((always_inline)) {
+    const int row0 = r_begin + fb * kLhRows;
+    const int valid = min(kLhRows, r_end - row0);
+    const int wbytes = static_cast<int>(((int64_t)(valid - 1) * a.ws + a.K) * sizeof(T));
+    pf_dma_tile_untracked<NIW_W, RPI, ROW_B, kLhWeightNt>(
+        wbase + (int64_t)row0 * a.ws, wbytes, (LC_LDS char*)wring[st], wave_s, woff, ft * ROW_B);
+    pf_dma_tile_untracked<NIW_H, RPI, ROW_B, false>(a.hidden, hbytes, (LC_LDS char*)hring[st],
+                                                    wave_s, hoff, ft * ROW_B);
   };
 
   f32x16_t acc[2];
@@ -182,85 +216,146 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-  auto compute = [&](auto st_c) __attribute__((always_inline)) {
-    LC_LDS const char* wl = wbuf(st_c) + wrow0;
-    LC_LDS const char* hl = hbuf(st_c);
+  auto compute = [&](int st) __attribute__((always_inline)) {
+    LC_LDS const char* wl = (LC_LDS const char*)wring[st] + wrow0;
+    LC_LDS const char* hl = (LC_LDS const char*)hring[st];
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       acc[s & 1] = Ops::mma(*reinterpret_cast<LC_LDS const v8*>(wl + raddr[s]),
                             *reinterpret_cast<LC_LDS const v8*>(hl + raddr[s]), acc[s & 1]);
   };
 
-  // Iteration t: wait for tile t (this wave's DMA; tile t+1 may still be in
-  // flight), barrier (every wave's part of tile t landed, every wave done with
-  // tile t-1), refill tile t-1's stage with tile t+2, compute tile t.
-  static_assert(kLhStages == 3, "the loop below is written for a three-stage ring");
-  // K a multiple of 128: with an odd number of half tiles the last tile's
-  // second half is past K, and its waves skip that tile's products.
-  const int n_tiles = (a.K + kLhKc - 1) / kLhKc;
-  const bool skip_last = kh == 1 && (a.K % kLhKc) != 0;
-  constexpr int kNi = NIW_W + NIW_H;  // DMA instructions per wave per tile
-  auto iteration = [&](int t, auto st_c) __attribute__((always_inline)) {
-    constexpr int S = decltype(st_c)::value;
-    if (t + 1 < n_tiles)
-      __builtin_amdgcn_s_waitcnt(lh_waitcnt(kNi, 0));
-    else
-      __builtin_amdgcn_s_waitcnt(lh_waitcnt(0, 0));
-    lc_compiler_fence();
-    __builtin_amdgcn_s_barrier();
-    lc_compiler_fence();
-    if (t + 2 < n_tiles) fetch(t + 2, std::integral_constant<int, (S + 2) % 3>{});
-    if (!(skip_last && t + 1 == n_tiles)) compute(st_c);
+  // At a block's end the second column half stores its sums in xch[block & 1]
+  // and the first half keeps its own in `keep`; after the next barrier the
+  // first half adds them up, rounds, and folds them into the lane's running
+  // best (batch row l32; the lane's vocab rows 8j + 4hh + i of its row group)
+  // as a packed key (lh_pack; 0 = none yet). Branch-free.
+  float keep[16];
+  unsigned long long best = 0;
+  auto block_epilogue = [&](int blk) __attribute__((always_inline)) {
+    if (kh == 0) {
+      const int row0 = r_begin + blk * kLhRows;
+      const int valid = min(kLhRows, r_end - row0);
+      const float* other = xch[blk & 1] + rw * 16 * 64 + lane;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = rw * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+        const float x = lc_to_f32(lc_from_f32<T>(keep[r] + other[r * 64]));
+        const unsigned long long k = lh_pack(x, row0 + row);
+        best = lh_max_key(best, row < valid ? k : 0ull);
+      }
+    }
+  };
+  auto block_end = [&](int blk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[0][r] += acc[1][r];
+    if (kh == 1) {
+      float* mine = xch[blk & 1] + rw * 16 * 64 + lane;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mine[r * 64] = acc[0][r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) keep[r] = acc[0][r];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
   };
 
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  fetch(0, I0{});
-  if (n_tiles > 1) fetch(1, I1{});
-  for (int t = 0; t < n_tiles; t += 3) {
-    iteration(t, I0{});
-    if (t + 1 < n_tiles) iteration(t + 1, I1{});
-    if (t + 2 < n_tiles) iteration(t + 2, I2{});
+  // Tile g = blk * n_tiles + t: wait for tile g (this wave's DMA; tile g+1
+  // may still be in flight), barrier (every wave's part of tile g landed,
+  // every wave done with tile g-1, the previous block's half sums stored),
+  // finish the previous block at its first tile, refill tile g-1's stage with
+  // tile g+2, compute tile g.
+  static_assert(kLhStages == 3, "the loop below is written for a three-stage ring");
+  // K a multiple of 128: with an odd number of half tiles each block's last
+  // tile's second half is past K, and its waves skip that tile's products.
+  const bool skip_last = kh == 1 && (a.K % kLhKc) != 0;
+  constexpr int kNi = NIW_W + NIW_H;  // DMA instructions per wave per tile
+  if (G > 0) fetch(0, 0, 0);
+  if (G > 1) fetch(n_tiles > 1 ? 0 : 1, n_tiles > 1 ? 1 : 0, 1);
+  int fb = n_tiles > 2 ? 0 : (n_tiles == 2 ? 1 : 2);  // tile 2 of the range
+  int ft = n_tiles > 2 ? 2 : 0;
+  int st = 0;
+  int g = 0;
+  for (int blk = 0; blk < nb; ++blk) {
+    for (int t = 0; t < n_tiles; ++t, ++g) {
+      if (g + 1 < G)
+        __builtin_amdgcn_s_waitcnt(lh_waitcnt(kNi, 0));
+      else
+        __builtin_amdgcn_s_waitcnt(lh_waitcnt(0, 0));
+      lc_compiler_fence();
+      __builtin_amdgcn_s_barrier();
+      lc_compiler_fence();
+      if (t == 0 && blk > 0) block_epilogue(blk - 1);
+      if (g + 2 < G) {
+        fetch(fb, ft, st == 0 ? 2 : st - 1);
+        if (++ft == n_tiles) {
+          ft = 0;
+          ++fb;
+        }
+      }
+      if (!(skip_last && t == n_tiles - 1)) compute(st);
+      st = st == 2 ? 0 : st + 1;
+    }
+    block_end(blk);
   }
-
-  // The second column half hands its sums to the first through LDS (the W
-  // ring is free after the barrier), added in a fixed order.
-#pragma unroll
-  for (int r = 0; r < 16; ++r) acc[0][r] += acc[1][r];
-  __syncthreads();
-  float* half = reinterpret_cast<float*>(w0);
-  if (kh == 1) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) half[(rw * 16 + r) * 64 + lane] = acc[0][r];
-  }
-  __syncthreads();
-  // Epilogue (first-half waves): lane (l32, hh) holds batch row l32 and vocab
-  // rows v0 + rw*32 + 8j + 4hh + i for register 4j + i.
-  float bv = -INFINITY;
-  int bi = INT_MAX;
+  __syncthreads();  // the last block's second-half sums are in LDS
+  if (nb > 0) block_epilogue(nb - 1);
+  // Workgroup best per batch row: the two lane halves, then the row groups
+  // through the exchange buffer the last block did not use (xch[nb & 1], free
+  // since the last barrier).
+  unsigned long long* red = reinterpret_cast<unsigned long long*>(xch[nb & 1]);
   if (kh == 0) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = rw * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-      const float x = lc_to_f32(lc_from_f32<T>(acc[0][r] + half[(rw * 16 + r) * 64 + lane]));
-      if (row < rows_valid) lh_take(bv, bi, x, v0 + row);
-    }
-    lh_take(bv, bi, __shfl_xor(bv, 32, 64), __shfl_xor(bi, 32, 64));
-    if (hh == 0) {
-      red_v[rw][l32] = bv;
-      red_i[rw][l32] = bi;
-    }
+    const uint32_t lo = static_cast<uint32_t>(best), hi = static_cast<uint32_t>(best >> 32);
+    best = lh_max_key(best, (static_cast<unsigned long long>(__shfl_xor(hi, 32, 64)) << 32) |
+                                __shfl_xor(lo, 32, 64));
+    if (hh == 0) red[rw * 32 + l32] = best;
   }
   __syncthreads();
   if (wave == 0 && hh == 0) {
 #pragma unroll
-    for (int w = 1; w < kLhRowWaves; ++w) lh_take(bv, bi, red_v[w][l32], red_i[w][l32]);
+    for (int w = 1; w < kLhRowWaves; ++w) best = lh_max_key(best, red[w * 32 + l32]);
+  }
+  if (a.keys == nullptr) {
+    if (wave == 0 && hh == 0 && l32 < a.B) {
+      a.part_val[(int64_t)blockIdx.x * a.pstride + l32] = lh_unpack_value(best);
+      a.part_idx[(int64_t)blockIdx.x * a.pstride + l32] = lh_unpack_index(best);
+    }
+    return;
+  }
+  // Merge into the packed keys; the workgroup that draws the last ticket
+  // (after every other workgroup's merges have been performed: returning
+  // atomics, waited for before the ticket) reads the keys back, resetting
+  // them, writes the ids, and returns the ticket to zero.
+  int& s_last = reinterpret_cast<int*>(red)[256];
+  if (wave == 0 && hh == 0 && l32 < a.B) {
+    const unsigned long long old = __hip_atomic_fetch_max(
+        a.keys + l32, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    (void)old;
+  }
+  __builtin_amdgcn_s_waitcnt(lh_waitcnt(0, 0));
+  __syncthreads();
+  if (tid == 0) {
+    unsigned* ticket = reinterpret_cast<unsigned*>(a.keys + kLhBatch);
+    const unsigned t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    s_last = t == static_cast<unsigned>(nwg - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (wave == 0 && hh == 0) {
+    const unsigned long long k =
+        __hip_atomic_exchange(a.keys + l32, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (l32 < a.B) {
-      a.part_val[(int64_t)blockIdx.x * a.pstride + l32] = bv;
-      a.part_idx[(int64_t)blockIdx.x * a.pstride + l32] = bi;
+      a.ids[l32] = lh_unpack_index(k);
+      if (a.max_out != nullptr) a.max_out[l32] = lh_unpack_value(k);
     }
   }
+  if (tid == 0)
+    __hip_atomic_store(reinterpret_cast<unsigned*>(a.keys + kLhBatch), 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One lane per vocab row; the hidden rows are read through the cache.
@@ -347,19 +442,21 @@ int run_lm_head(LhArgs a, bool mfma, int64_t* ids, float* max_out, hipStream_t s
 
 template <typename T>
 int run_lm_head_mfma(LhArgs a, int64_t* ids, float* max_out, hipStream_t st) {
-  {
-    const int n_wg = (a.V + kLhRows - 1) / kLhRows;
-    const T* hidden = static_cast<const T*>(a.hidden);
-    const int B = a.B;
-    a.pstride = kLhBatch;
-    for (int b0 = 0; b0 < B; b0 += kLhBatch) {
-      a.hidden = hidden + (int64_t)b0 * a.hs;
-      a.B = min(kLhBatch, B - b0);
-      lm_head_argmax_mfma_kernel<T><<<n_wg, 64 * kLhWaves, 0, st>>>(a);
+  // One workgroup per CU (its 160 KiB of LDS), each over V / grid rows.
+  const int n_wg = static_cast<int>(std::min<int64_t>((a.V + kLhRows - 1) / kLhRows,
+                                                      lc_cu_count()));
+  const T* hidden = static_cast<const T*>(a.hidden);
+  const int B = a.B;
+  a.pstride = kLhBatch;
+  for (int b0 = 0; b0 < B; b0 += kLhBatch) {
+    a.hidden = hidden + (int64_t)b0 * a.hs;
+    a.B = min(kLhBatch, B - b0);
+    a.ids = ids + b0;
+    a.max_out = max_out ? max_out + b0 : nullptr;
+    lm_head_argmax_mfma_kernel<T><<<n_wg, 64 * kLhWaves, 0, st>>>(a);
+    if (a.keys == nullptr)
       lm_head_argmax_reduce_kernel<<<a.B, 1024, 0, st>>>(a.part_val, a.part_idx, n_wg, a.pstride,
-                                                          ids + b0,
-                                                          max_out ? max_out + b0 : nullptr);
-    }
+                                                          a.ids, a.max_out);
   }
   return lc_check_launch("lc_lm_head_argmax");
 }
@@ -367,6 +464,8 @@ int run_lm_head_mfma(LhArgs a, int64_t* ids, float* max_out, hipStream_t st) {
 }  // namespace
 
 extern "C" {
+
+int64_t lc_lm_head_argmax_counter_count() { return kLhCounterInts; }
 
 int64_t lc_lm_head_argmax_workspace_bytes(int64_t B, int64_t V) {
   if (B < 0 || V < 0) return -1;
@@ -377,8 +476,8 @@ int64_t lc_lm_head_argmax_workspace_bytes(int64_t B, int64_t V) {
 
 int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void* weight,
                       int64_t weight_row_stride, int64_t B, int64_t K, int64_t V, int64_t* ids,
-                      float* max_logit, void* workspace, int64_t workspace_bytes, int dtype,
-                      void* stream) {
+                      float* max_logit, void* workspace, int64_t workspace_bytes,
+                      int32_t* counters, int dtype, void* stream) {
   if (B == 0) return LC_OK;  // no rows (pointers may be null)
   LC_REQUIRE(hidden && weight && ids && workspace, "lc_lm_head_argmax: null pointer");
   LC_REQUIRE(B >= 0 && B < 65536, "lc_lm_head_argmax: batch %lld out of range", (long long)B);
@@ -390,6 +489,8 @@ int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void*
   LC_REQUIRE(workspace_bytes >= need, "lc_lm_head_argmax: workspace %lld < %lld bytes",
              (long long)workspace_bytes, (long long)need);
   LC_REQUIRE(lc_aligned(workspace, 16), "lc_lm_head_argmax: workspace not 16-byte aligned");
+  LC_REQUIRE(counters == nullptr || lc_aligned(counters, 8),
+             "lc_lm_head_argmax: counters not 8-byte aligned");
   if (B == 0) return LC_OK;
   const int64_t parts = (V + kLhRows - 1) / kLhRows;
   LhArgs a{};
@@ -398,6 +499,9 @@ int lc_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, const void*
   a.part_val = static_cast<float*>(workspace);
   a.part_idx = reinterpret_cast<int*>(static_cast<char*>(workspace) +
                                       parts * (B > kLhBatch ? B : kLhBatch) * 4);
+  // The fused argmax (packed keys + ticket) runs on the MFMA path only; the
+  // generic kernel always hands partials to the reduce kernel.
+  a.keys = reinterpret_cast<unsigned long long*>(counters);
   a.hs = hidden_row_stride;
   a.ws = weight_row_stride;
   a.B = (int)B;

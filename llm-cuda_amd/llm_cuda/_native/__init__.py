@@ -67,10 +67,11 @@ _SIGNATURES = {
          _c_i64, _c_p, _c_i64p, ctypes.c_int, ctypes.c_float, _c_p, _c_i64, ctypes.c_int, _c_p],
     ),
     "lc_lm_head_argmax_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "lc_lm_head_argmax_counter_count": (_c_i64, []),
     "lc_lm_head_argmax": (
         ctypes.c_int,
-        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, ctypes.c_int,
-         _c_p],
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p,
+         ctypes.c_int, _c_p],
     ),
     "lc_decode_linear_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int]),
     "lc_decode_linear_counter_count": (_c_i64, [_c_i64, ctypes.c_int]),

@@ -481,11 +481,12 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
     lib = nat.load()
     ws_bytes = lib.lc_lm_head_argmax_workspace_bytes(B, V)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    counters = _zeroed_counters("lm_head", dev, lib.lc_lm_head_argmax_counter_count())
     with _DeviceGuard(dev):
         rc = lib.lc_lm_head_argmax(
             hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0), B, K, V,
             ids.data_ptr(), None if mx is None else mx.data_ptr(), ws.data_ptr(), ws.numel(),
-            nat.lc_dtype(hidden), _stream(dev))
+            counters.data_ptr(), nat.lc_dtype(hidden), _stream(dev))
     nat.check(rc, "lc_lm_head_argmax")
     return (ids, mx) if return_max else ids
 
@@ -496,35 +497,41 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_max: bool 
 # ---------------------------------------------------------------------------
 DECODE_LINEAR_MAX_ROWS = 32
 _NATIVE_PROJECTIONS = [True]
-_DL_COUNTERS: dict = {}
+_COUNTERS: dict = {}
 # Counter buffers replaced by a larger one stay referenced here: a HIP graph
 # captured earlier may still hold their addresses.
-_DL_RETIRED: list = []
+_RETIRED_COUNTERS: list = []
+
+
+def _zeroed_counters(kind: str, dev: torch.device, n: int) -> torch.Tensor:
+    """Zeroed int32 counters for the kernels that take them (`kind`:
+    "decode_linear" ticket counters, "lm_head" argmax keys and ticket). Each
+    call leaves its counters at zero, so calls that follow one another on a
+    stream can share a buffer; calls on different streams (which may overlap)
+    must not. Eager calls get one buffer per (kind, device, stream). Calls
+    captured into HIP graphs share one more buffer per (kind, device) (a
+    capture cannot allocate and zero it: every eager call makes sure it
+    exists), so replays of graphs holding such calls must not overlap on one
+    device."""
+    capturing = torch.cuda.is_current_stream_capturing()
+    keys = [(kind, dev.type, dev.index, "graphs")]
+    if not capturing:
+        keys.append((kind, dev.type, dev.index, _stream(dev)))
+    for key in keys:
+        buf = _COUNTERS.get(key)
+        if buf is None or buf.numel() < n:
+            if capturing:
+                raise RuntimeError(f"{kind}: run one call outside graph capture first "
+                                   "(its counters are allocated and zeroed eagerly)")
+            if buf is not None:
+                _RETIRED_COUNTERS.append(buf)
+            buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
+            _COUNTERS[key] = buf
+    return buf
 
 
 def _decode_linear_counters(dev: torch.device, n: int) -> torch.Tensor:
-    """Zeroed int32 ticket counters for lc_decode_linear. Each call returns its
-    counters to zero, so calls that follow one another on a stream can share a
-    buffer; calls on different streams (which may overlap) must not. Eager
-    calls get one buffer per (device, stream). Calls captured into HIP graphs
-    share one more buffer per device (a capture cannot allocate and zero it:
-    every eager call makes sure it exists), so replays of graphs holding
-    decode_linear calls must not overlap on one device."""
-    capturing = torch.cuda.is_current_stream_capturing()
-    keys = [(dev.type, dev.index, "graphs")]
-    if not capturing:
-        keys.append((dev.type, dev.index, _stream(dev)))
-    for key in keys:
-        buf = _DL_COUNTERS.get(key)
-        if buf is None or buf.numel() < n:
-            if capturing:
-                raise RuntimeError("decode_linear: run one call outside graph capture first "
-                                   "(its ticket counters are allocated and zeroed eagerly)")
-            if buf is not None:
-                _DL_RETIRED.append(buf)
-            buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
-            _DL_COUNTERS[key] = buf
-    return buf
+    return _zeroed_counters("decode_linear", dev, n)
 
 
 @contextlib.contextmanager

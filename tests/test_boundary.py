@@ -325,13 +325,15 @@ def test_every_entry_accepts_empty_work_with_null_pointers():
     assert lib.lc_swiglu_fwd(None, None, None, 0, 8, 8, 8, 8, 2, None) == 0
     assert lib.lc_rope_fwd(None, None, 1, st, st, None, None, 0, None, None, None, None, 8, 8, 0,
                            4, 8, 2, None) == 0
-    assert lib.lc_lm_head_argmax(None, 8, None, 8, 0, 8, 8, None, None, None, 0, 2, None) == 0
+    assert lib.lc_lm_head_argmax(None, 8, None, 8, 0, 8, 8, None, None, None, 0, None, 2,
+                                 None) == 0
     assert lib.lc_prefill_attn_bwd(None, None, None, None, None, None, None, None, None, 0, 4, 2,
                                    8, 8, 64, st, st, st, st, st, st, st, st, 0, None, None, 0, 1.0,
                                    None, 0, 2, None) == 0
     # a null pointer behind real work is still an error
     assert lib.lc_swiglu_fwd(None, None, None, 2, 8, 8, 8, 8, 2, None) == -1
-    assert lib.lc_lm_head_argmax(None, 8, None, 8, 2, 8, 8, None, None, None, 4096, 2, None) == -1
+    assert lib.lc_lm_head_argmax(None, 8, None, 8, 2, 8, 8, None, None, None, 4096, None, 2,
+                                 None) == -1
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

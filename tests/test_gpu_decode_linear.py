@@ -132,7 +132,7 @@ def test_consecutive_calls_reuse_workspace_and_counters():
         _check(y, _ref(x, w, False), 1.0)
     torch.cuda.synchronize()
     dev = torch.device("cuda", torch.cuda.current_device())
-    counters = _ops._DL_COUNTERS[("cuda", dev.index, _ops._stream(dev))]
+    counters = _ops._COUNTERS[("decode_linear", "cuda", dev.index, _ops._stream(dev))]
     assert int(counters.abs().sum()) == 0
 
 
@@ -152,8 +152,8 @@ def test_counters_are_per_stream_and_odd_widths_route_elsewhere():
     torch.cuda.synchronize()
     assert torch.equal(y0, y1)
     dev = torch.device("cuda", torch.cuda.current_device())
-    main = _ops._DL_COUNTERS[("cuda", dev.index, _ops._stream(dev))]
-    other = _ops._DL_COUNTERS[("cuda", dev.index, side.cuda_stream)]
+    main = _ops._COUNTERS[("decode_linear", "cuda", dev.index, _ops._stream(dev))]
+    other = _ops._COUNTERS[("decode_linear", "cuda", dev.index, side.cuda_stream)]
     assert main.data_ptr() != other.data_ptr()
     assert _ops.decode_linear_applies(x, w)
     assert not _ops.decode_linear_applies(x, w[:510])  # N = 510

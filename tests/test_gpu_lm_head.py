@@ -109,3 +109,61 @@ def test_lm_head_argmax_rejects_bad_shapes(cuda):
         _ops.lm_head_argmax(h, torch.zeros(10, 64, device=cuda, dtype=torch.bfloat16))
     with pytest.raises(TypeError):
         _ops.lm_head_argmax(h, torch.zeros(10, 128, device=cuda, dtype=torch.float16))
+
+
+def _abi_call(hidden, weight, counters):
+    from llm_cuda import _native
+
+    lib = _native.load()
+    B, K = hidden.shape
+    V = weight.shape[0]
+    ids = torch.full((B,), -7, dtype=torch.int64, device=hidden.device)
+    mx = torch.full((B,), float("nan"), dtype=torch.float32, device=hidden.device)
+    ws = torch.empty(max(lib.lc_lm_head_argmax_workspace_bytes(B, V), 16), dtype=torch.uint8,
+                     device=hidden.device)
+    rc = lib.lc_lm_head_argmax(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
+                               weight.stride(0), B, K, V, ids.data_ptr(), mx.data_ptr(),
+                               ws.data_ptr(), ws.numel(),
+                               None if counters is None else counters.data_ptr(),
+                               _native.lc_dtype(hidden), torch.cuda.current_stream().cuda_stream)
+    _native.check(rc, "lc_lm_head_argmax")
+    return ids, mx
+
+
+@pytest.mark.parametrize("B,K,V", [(1, 128, 10), (32, 4096, 20000), (33, 512, 3000),
+                                   (7, 256, 16385), (4, 1024, 64)])
+def test_lm_head_fused_select_matches_reduce_launch(cuda, B, K, V):
+    """The MFMA path's in-kernel selection (packed keys + ticket, with a
+    counters buffer) gives the ids and logits of its partials + reduce-launch
+    form, call after call, and leaves the counters at zero. Rows of zeros
+    (every logit +-0: the smallest index wins), copied winners (ties) and a
+    NaN row are included."""
+    from llm_cuda import _native
+
+    lib = _native.load()
+    g = torch.Generator().manual_seed(B + K + V)
+    hidden = torch.randn(B, K, generator=g).bfloat16()
+    weight = (torch.randn(V, K, generator=g) * 0.02).bfloat16()
+    hidden[0] = 0.0
+    if V > 100:
+        weight[V // 2] = weight[V // 3]
+        weight[V - 1] = weight[7]
+    if B > 2:
+        hidden[1] = -hidden[2]
+    hidden, weight = hidden.to(cuda), weight.to(cuda)
+    n = lib.lc_lm_head_argmax_counter_count()
+    counters = torch.zeros(n, dtype=torch.int32, device=cuda)
+    ref_ids, ref_mx = _abi_call(hidden, weight, None)
+    for call in range(3):
+        ids, mx = _abi_call(hidden, weight, counters)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ref_ids), f"call {call}: ids differ"
+        assert torch.equal(mx, ref_mx), f"call {call}: winning logits differ"
+        assert not counters.any(), f"call {call}: counters not returned to zero"
+    assert int(ref_ids[0]) == 0
+    if V > 100:
+        nan_w = weight.clone()
+        nan_w[V // 4, 3] = float("nan")
+        ids_n, _ = _abi_call(hidden, nan_w, counters)
+        assert (ids_n.cpu() == V // 4).all()
+        assert not counters.any()
