@@ -143,7 +143,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(PrefillArgs a) {
 // the reference max as it stands, and a check between part A and part B
 // (every lane's tile sum <= 2^8, which holds whenever every p <= 2^8) sends
 // the rare tiles that fail it through a fix-up that takes their row max from
-// the exponents and rescales before their PV. The max tree and its ballot
+// the exponents and rescales every row that grew before their PV. The max tree and its ballot
 // leave the loop (about a fifth of its non-exp VALU work).
 // LDS holds two K and two V tile buffers as separate arrays. Iteration t reads
 // K(t+1), V(t) and fetches K(t+2), V(t+1) by buffer-to-LDS DMA into the other
@@ -416,8 +416,8 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   // the current reference max, SM2L exponentiates and sums, and check_fix
   // catches every tile where some p exceeds 2^8 (its lane's tile sum then
   // does too): that tile's row max is taken from its exponents, and rows
-  // whose max is above the threshold move their reference max there (O and
-  // l rescaled, the tile's p recomputed) before the tile's PV.
+  // whose max grew move their reference max there (O and l rescaled, the
+  // tile's p recomputed) before the tile's PV.
   auto sm1l = [&](int k0, auto mask_c) __attribute__((always_inline)) {
     if constexpr (decltype(mask_c)::value) {
 #pragma unroll
@@ -453,7 +453,12 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, xcu[kt][r]);
       mx = pf_half_max(mx);
-      const float d = mx > kPfRescaleLog2 ? mx : 0.f;
+      // Every row whose max grew moves its reference max there (as the
+      // max-tree path does once any row passes the threshold), so after a
+      // fix every row's largest p is 1: leaving rows below the threshold
+      // where they were measured less accurate on scores that climb steadily
+      // (a larger O error, and one that the backward's dq then amplifies).
+      const float d = mx > 0.f ? mx : 0.f;
       const float al = lc_exp2(-d);
       m_ref += d;
       l_lane *= al;
