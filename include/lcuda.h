@@ -263,6 +263,9 @@ LC_API int lc_decode_linear_partials(const void* x, int64_t x_row_stride, const 
  * (partial outputs and logsumexps of every split). */
 LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits);
 
+/* Number of int32 counters lc_paged_decode_fwd takes (its counters argument). */
+LC_API int64_t lc_paged_decode_counter_count(void);
+
 /* Split-K paged GQA flash-decode: one query token per sequence against the
  * K/V pages named by the block table, then a cross-split logsumexp merge.
  * out[b,h,:] = softmax(q[b,h,:].K_b^T * scale) V_b over the seq_lens[b] tokens
@@ -294,16 +297,24 @@ LC_API int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D,
  *   tokens evenly among its waves and merges them in LDS, with no merge
  *   launch; it suits batches of equal lengths whose units (sequences x kv
  *   heads x head groups) fill whole rounds of the CUs.
- * workspace: >= lc_paged_decode_workspace_bytes(B, Hq, D, max_splits). */
+ * workspace: >= lc_paged_decode_workspace_bytes(B, Hq, D, max_splits).
+ * counters: lc_paged_decode_counter_count() int32 values that are zero at
+ *   entry and are left zero, or NULL. Ragged batches whose splits take more
+ *   than one round of the CUs run in a longest-first order of (sequence,
+ *   split) pairs; with counters, its last quarter is handed out to the
+ *   workgroups in the order they start (the XCDs read at different rates),
+ *   with NULL the order is static. The outputs are the same either way.
+ *   Calls that may overlap (other streams) need their own counters. */
 LC_API int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* key_pages,
                         const void* value_pages, int64_t kv_s_page, int64_t kv_s_head,
                         int64_t kv_s_tok, const int32_t* block_table, int64_t bt_stride,
                         int64_t max_pages_per_seq, int64_t num_pages, const int32_t* seq_lens,
                         void* out, int64_t o_sb, int64_t o_sh, float* lse, const void* bias,
                         int64_t bias_sb, int64_t bias_sh, int64_t bias_len, int bias_dtype,
-                        void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
-                        int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
-                        int64_t max_splits, float scale, int dtype, void* stream);
+                        void* workspace, int64_t workspace_bytes, int32_t* counters, int64_t B,
+                        int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                        int64_t split_tokens, int64_t max_splits, float scale, int dtype,
+                        void* stream);
 
 /* Size of the device scratch behind lc_paged_decode_fwd_noalloc: the largest
  * lc_paged_decode_workspace_bytes(B, Hq, D, max_splits) it accepts (32 MiB:
@@ -318,7 +329,8 @@ LC_API int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const 
  * capture, serving loops and harnesses that forbid hipMalloc). It allocates
  * nothing and calls no allocating routine; the first call on a device looks
  * up that device's copy of the array once. Semantics and arguments are those
- * of lc_paged_decode_fwd; the stream must belong to the current device.
+ * of lc_paged_decode_fwd with NULL counters (the static order); the stream
+ * must belong to the current device.
  * Returns LC_EWORKSPACE (no launch) when the partials of (B, Hq, D,
  * max_splits) exceed the scratch. Every call on one GPU shares its scratch:
  * calls that overlap on that GPU (other streams or threads) race and must be

@@ -53,6 +53,11 @@ struct DecodeArgs {
   const void* bias;
   int64_t bias_sb, bias_sh;
   int bias_len, bias_dtype;
+  // Longest-first order (ORD): a ticket that is zero at entry and left zero,
+  // or null (every workgroup keeps rank = its block id); ord_static: the
+  // workgroups below this block id always keep their id as rank.
+  int* ord_ticket;
+  int ord_static;
 };
 
 // Bias of token tok for (b, h), in the exp2 domain; 0 past bias_len.
@@ -485,18 +490,46 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
 }
 
 constexpr int kOrdChunks = 4;
-__device__ __forceinline__ int ordered_pair_chunked(const DecodeArgs& a, int r, int lane,
+// int32 counters lc_paged_decode_fwd takes: the ticket, padded to 256 bytes.
+constexpr int kDecodeCounterInts = 64;
+
+// The batch's lengths for the order, sequence 64c + lane in li[c] (0 past B).
+__device__ __forceinline__ void ord_lengths(const DecodeArgs& a, int lane,
+                                            int (&li)[kOrdChunks]) {
+  const int nc = (a.B + 63) >> 6;
+#pragma unroll
+  for (int c = 0; c < kOrdChunks; ++c) {
+    const int bi = c * 64 + lane;
+    li[c] = c < nc && bi < a.B ? seq_len_of(a, bi) : 0;
+  }
+}
+
+// Number of (sequence, split) pairs with tokens: every whole split and every
+// final partial split (wave-uniform).
+__device__ __forceinline__ int ord_pair_count(const DecodeArgs& a, const int (&li)[kOrdChunks]) {
+  const int nc = (a.B + 63) >> 6;
+  int n = 0;
+#pragma unroll
+  for (int c = 0; c < kOrdChunks; ++c) {
+    if (c >= nc) break;
+    const int whole = li[c] / a.split_tokens;
+    n += __builtin_amdgcn_readlane(wave_incl_scan(whole), 63) +
+         __popcll(__ballot(li[c] - whole * a.split_tokens > 0));
+  }
+  return n;
+}
+
+__device__ __forceinline__ int ordered_pair_chunked(const DecodeArgs& a,
+                                                    const int (&li)[kOrdChunks], int r, int lane,
                                                     int& len_out) {
   const int nc = (a.B + 63) >> 6;  // chunks in use (uniform)
   // Chunks past nc hold no sequence; every loop below skips them (uniform
   // branches), so a batch of <= 64 pays for one chunk only.
-  int li[kOrdChunks] = {}, whole[kOrdChunks] = {}, rem[kOrdChunks] = {}, incl[kOrdChunks] = {};
+  int whole[kOrdChunks] = {}, rem[kOrdChunks] = {}, incl[kOrdChunks] = {};
   int carry = 0;  // whole splits of the earlier chunks
 #pragma unroll
   for (int c = 0; c < kOrdChunks; ++c) {
     if (c >= nc) break;
-    const int bi = c * 64 + lane;
-    li[c] = bi < a.B ? seq_len_of(a, bi) : 0;
     whole[c] = li[c] / a.split_tokens;
     rem[c] = li[c] - whole[c] * a.split_tokens;
     incl[c] = wave_incl_scan(whole[c]) + carry;  // prefix sum of the whole splits
@@ -566,8 +599,8 @@ __device__ __forceinline__ int ordered_pair_chunked(const DecodeArgs& a, int r, 
 // The same order for B <= 64 (one sequence per lane): the batches this path
 // was first measured on take the shorter code (the chunked form measured ~1%
 // slower at 64 sequences).
-__device__ __forceinline__ int ordered_pair_64(const DecodeArgs& a, int r, int lane, int& len_out) {
-  const int li = lane < a.B ? seq_len_of(a, lane) : 0;
+__device__ __forceinline__ int ordered_pair_64(const DecodeArgs& a, int li, int r, int lane,
+                                               int& len_out) {
   const int whole = li / a.split_tokens;
   const int rem = li - whole * a.split_tokens;
   const int incl = wave_incl_scan(whole);  // inclusive prefix sum of the whole splits
@@ -599,9 +632,10 @@ __device__ __forceinline__ int ordered_pair_64(const DecodeArgs& a, int r, int l
   return (bb << 16) | sp;
 }
 
-__device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane, int& len_out) {
-  return a.B <= 64 ? ordered_pair_64(a, r, lane, len_out)
-                   : ordered_pair_chunked(a, r, lane, len_out);
+__device__ __forceinline__ int ordered_pair(const DecodeArgs& a, const int (&li)[kOrdChunks],
+                                            int r, int lane, int& len_out) {
+  return a.B <= 64 ? ordered_pair_64(a, li[0], r, lane, len_out)
+                   : ordered_pair_chunked(a, li, r, lane, len_out);
 }
 
 // Single-split decode (max_splits == 1) for page_size % 32 == 0: one
@@ -627,9 +661,13 @@ __device__ __forceinline__ int ordered_pair(const DecodeArgs& a, int r, int lane
 // append and decode launches in sequence, up to fp32 summation order.
 //
 // ORD (several splits, B <= 256, not STEP): a one-dimensional grid whose
-// workgroup i takes unit i % (Hkv * n_hgroups) of pair i / (Hkv * n_hgroups)
-// in the order of ordered_pair; the splits and their partials are the same
-// as in the (units, B, splits) grid.
+// workgroup of rank i takes unit i % (Hkv * n_hgroups) of pair
+// i / (Hkv * n_hgroups) in the order of ordered_pair; the splits and their
+// partials are the same as in the (units, B, splits) grid. The rank is the
+// block id, except that with a ticket (ord_ticket) the last quarter of the
+// live ranks is handed out in the order the workgroups start, so the faster
+// XCDs take more of the short final splits (which workgroup computes a split
+// changes nothing in its partials).
 template <typename T, int DPAD, bool HB, bool STEP, bool PRE, bool ORD = false>
 __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_cluster_kernel(
     DecodeArgs a, T* __restrict__ out, int64_t o_sb, int64_t o_sh, float* __restrict__ lse_out,
@@ -654,9 +692,36 @@ __global__ __launch_bounds__(64 * cluster_waves<DPAD>()) void paged_decode_clust
   int kvh, hg, b, split, ord_len = 0;
   if constexpr (ORD) {
     const int units = a.Hkv * a.n_hgroups;
-    const int r = blockIdx.x / units;
-    const int u = blockIdx.x - r * units;
-    const int pair = ordered_pair(a, r, lane, ord_len);
+    int li[kOrdChunks];
+    ord_lengths(a, lane, li);
+    int rank = blockIdx.x;
+    if (a.ord_ticket != nullptr) {
+      // Dynamic tail: the XCDs read at different rates, so the last quarter
+      // of the live workgroups' ranks (the shortest splits) go to whichever
+      // workgroups start first, through the ticket. A spare pool of an eighth
+      // more workgroups lets the faster XCDs take more of them; workgroups
+      // past it leave at once. Every workgroup in [s0, n_draw) draws exactly
+      // once, so the one that draws the last value returns the ticket to zero.
+      const int n_live = ord_pair_count(a, li) * units;
+      const int s0 = max(min((int)gridDim.x, a.ord_static), n_live - (n_live >> 2));
+      const int n_draw = max(s0, min((int)gridDim.x, n_live + (n_live >> 3)));
+      if (rank >= n_draw) return;
+      if (rank >= s0) {
+        __shared__ int s_rank;
+        if (threadIdx.x == 0) {
+          const int t = __hip_atomic_fetch_add(a.ord_ticket, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+          if (t == n_draw - s0 - 1)
+            __hip_atomic_store(a.ord_ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          s_rank = s0 + t;
+        }
+        __syncthreads();
+        rank = s_rank;
+      }
+    }
+    const int r = rank / units;
+    const int u = rank - r * units;
+    const int pair = ordered_pair(a, li, r, lane, ord_len);
     if (pair < 0) return;
     kvh = u / a.n_hgroups;
     hg = u - kvh * a.n_hgroups;
@@ -1308,9 +1373,10 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
                       int64_t bt_stride, int64_t max_pages_per_seq, int64_t num_pages,
                       const int32_t* seq_lens, void* out, int64_t o_sb, int64_t o_sh, float* lse,
                       const void* bias, int64_t bias_sb, int64_t bias_sh, int64_t bias_len,
-                      int bias_dtype, void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
-                      int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
-                      int64_t max_splits, float scale, int dtype, void* stream) {
+                      int bias_dtype, void* workspace, int64_t workspace_bytes, int32_t* counters,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                      int64_t split_tokens, int64_t max_splits, float scale, int dtype,
+                      void* stream) {
   LC_REQUIRE((q && key_pages && value_pages && block_table && seq_lens && out && workspace) ||
                  B == 0,
              "%s: null pointer", who);
@@ -1334,6 +1400,7 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
   LC_REQUIRE(workspace_bytes >= need, "%s: workspace %lld < %lld bytes", who,
              (long long)workspace_bytes, (long long)need);
   LC_REQUIRE(lc_aligned(workspace, 256), "%s: workspace not 256-byte aligned", who);
+  LC_REQUIRE(lc_aligned(counters, 4), "%s: counters not 4-byte aligned", who);
   LC_REQUIRE(bias == nullptr || (bias_sb >= 0 && bias_sh >= 0 && bias_len >= 0 &&
                                  bias_len < (1LL << 31)),
              "%s: bad bias strides or length", who);
@@ -1376,6 +1443,8 @@ int paged_decode_impl(const char* who, const void* q, int64_t q_sb, int64_t q_sh
   a.bias_sh = bias_sh;
   a.bias_len = static_cast<int>(bias_len);
   a.bias_dtype = bias_dtype;
+  a.ord_ticket = counters;
+  a.ord_static = lc_cu_count();
 
   const int esz = lc_dtype_size(dtype);
   const bool half = dtype == LC_DTYPE_BF16 || dtype == LC_DTYPE_F16;
@@ -1589,6 +1658,8 @@ int scratch_for_stream(const char* who, void* stream, void** out) {
 
 extern "C" {
 
+int64_t lc_paged_decode_counter_count(void) { return kDecodeCounterInts; }
+
 int64_t lc_paged_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t max_splits) {
   if (B < 0 || Hq < 0 || D < 0 || max_splits < 0) return -1;
   const int64_t n = B * Hq * max_splits;
@@ -1603,14 +1674,16 @@ int lc_paged_decode_fwd(const void* q, int64_t q_sb, int64_t q_sh, const void* k
                         int64_t max_pages_per_seq, int64_t num_pages, const int32_t* seq_lens,
                         void* out, int64_t o_sb, int64_t o_sh, float* lse, const void* bias,
                         int64_t bias_sb, int64_t bias_sh, int64_t bias_len, int bias_dtype,
-                        void* workspace, int64_t workspace_bytes, int64_t B, int64_t Hq,
-                        int64_t Hkv, int64_t D, int64_t page_size, int64_t split_tokens,
-                        int64_t max_splits, float scale, int dtype, void* stream) {
+                        void* workspace, int64_t workspace_bytes, int32_t* counters,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                        int64_t split_tokens, int64_t max_splits, float scale, int dtype,
+                        void* stream) {
   return paged_decode_impl("lc_paged_decode_fwd", q, q_sb, q_sh, key_pages, value_pages,
                            kv_s_page, kv_s_head, kv_s_tok, block_table, bt_stride,
                            max_pages_per_seq, num_pages, seq_lens, out, o_sb, o_sh, lse, bias,
-                           bias_sb, bias_sh, bias_len, bias_dtype, workspace, workspace_bytes, B,
-                           Hq, Hkv, D, page_size, split_tokens, max_splits, scale, dtype, stream);
+                           bias_sb, bias_sh, bias_len, bias_dtype, workspace, workspace_bytes,
+                           counters, B, Hq, Hkv, D, page_size, split_tokens, max_splits, scale,
+                           dtype, stream);
 }
 
 int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
@@ -1637,12 +1710,13 @@ int lc_paged_decode_fwd_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
   const int rc = scratch_for_stream(who, stream, &ws);
   if (rc != LC_OK) return rc;
   // No part of the scratch needs clearing: every split with tokens writes its
-  // partials, and the merge reads only those splits.
+  // partials, and the merge reads only those splits. No ticket either (the
+  // static longest-first order), so nothing here has to start at zero.
   return paged_decode_impl(who, q, q_sb, q_sh, key_pages, value_pages, kv_s_page, kv_s_head,
                            kv_s_tok, block_table, bt_stride, max_pages_per_seq, num_pages,
                            seq_lens, out, o_sb, o_sh, lse, bias, bias_sb, bias_sh, bias_len,
-                           bias_dtype, ws, LC_DECODE_NOALLOC_SCRATCH_BYTES, B, Hq, Hkv, D,
-                           page_size, split_tokens, max_splits, scale, dtype, stream);
+                           bias_dtype, ws, LC_DECODE_NOALLOC_SCRATCH_BYTES, nullptr, B, Hq,
+                           Hkv, D, page_size, split_tokens, max_splits, scale, dtype, stream);
 }
 
 int lc_paged_decode_step(const void* q, int64_t q_sb, int64_t q_sh, const void* k,

@@ -92,11 +92,12 @@ _SIGNATURES = {
          _c_i64, ctypes.c_float, ctypes.c_int, ctypes.c_int, _c_p],
     ),
     "lc_paged_decode_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "lc_paged_decode_counter_count": (_c_i64, []),
     "lc_paged_decode_fwd": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
          _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_p,
-         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
+         _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
          ctypes.c_int, _c_p],
     ),
     "lc_paged_decode_fwd_noalloc": (

@@ -503,16 +503,18 @@ _COUNTERS: dict = {}
 _RETIRED_COUNTERS: list = []
 
 
-def _zeroed_counters(kind: str, dev: torch.device, n: int) -> torch.Tensor:
+def _zeroed_counters(kind: str, dev: torch.device, n: int, optional: bool = False):
     """Zeroed int32 counters for the kernels that take them (`kind`:
-    "decode_linear" ticket counters, "lm_head" argmax keys and ticket). Each
+    "decode_linear" ticket counters, "lm_head" argmax keys and ticket,
+    "paged_decode" the ticket of the longest-first order's dynamic tail). Each
     call leaves its counters at zero, so calls that follow one another on a
     stream can share a buffer; calls on different streams (which may overlap)
     must not. Eager calls get one buffer per (kind, device, stream). Calls
     captured into HIP graphs share one more buffer per (kind, device) (a
     capture cannot allocate and zero it: every eager call makes sure it
     exists), so replays of graphs holding such calls must not overlap on one
-    device."""
+    device. A capture before any eager call raises, or returns None when
+    `optional` (for kernels whose counters are an optimisation only)."""
     capturing = torch.cuda.is_current_stream_capturing()
     keys = [(kind, dev.type, dev.index, "graphs")]
     if not capturing:
@@ -521,6 +523,8 @@ def _zeroed_counters(kind: str, dev: torch.device, n: int) -> torch.Tensor:
         buf = _COUNTERS.get(key)
         if buf is None or buf.numel() < n:
             if capturing:
+                if optional:
+                    return None
                 raise RuntimeError(f"{kind}: run one call outside graph capture first "
                                    "(its counters are allocated and zeroed eagerly)")
             if buf is not None:
@@ -864,6 +868,10 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
         bias = decode_bias(attention_mask, B, Hq, q4.dtype)
     out = torch.empty((B, Hq, 1, D), dtype=q4.dtype, device=dev)
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if return_lse else None
+    # The ticket of the longest-first order's dynamic tail (zero-on-exit); a
+    # capture before any eager call runs the static order (no counters).
+    counters = _zeroed_counters("paged_decode", dev, lib.lc_paged_decode_counter_count(),
+                                optional=True)
     with _DeviceGuard(dev):
         rc = lib.lc_paged_decode_fwd(
             q4.data_ptr(), q4.stride(0), q4.stride(1), key_pages.data_ptr(),
@@ -874,8 +882,9 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
             None if bias is None else bias.data_ptr(), 0 if bias is None else bias.stride(0),
             0 if bias is None else bias.stride(1), 0 if bias is None else bias.shape[-1],
             0 if bias is None else nat.lc_dtype(bias), workspace.data_ptr(),
-            workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, P, split_tokens,
-            max_splits, float(scale), nat.lc_dtype(q4), _stream(dev))
+            workspace.numel() * workspace.element_size(),
+            None if counters is None else counters.data_ptr(), B, Hq, Hkv, D, P,
+            split_tokens, max_splits, float(scale), nat.lc_dtype(q4), _stream(dev))
     nat.check(rc, "lc_paged_decode_fwd")
     if squeeze:
         out = out.squeeze(2)

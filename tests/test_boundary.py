@@ -103,17 +103,18 @@ def test_invalid_arguments_rejected_before_launch():
     assert rc == -1 and b"even" in lib.lc_last_error()
     # split does not cover the table capacity
     rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
-                                 None, 0, 0, 0, 0, 256, 1 << 20, 1, 4, 2, 128, 64, 64, 1, 1.0, 2,
-                                 None)
+                                 None, 0, 0, 0, 0, 256, 1 << 20, None, 1, 4, 2, 128, 64, 64, 1,
+                                 1.0, 2, None)
     assert rc == -1 and b"capacity" in lib.lc_last_error()
     # workspace too small
     rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
-                                 None, 0, 0, 0, 0, 256, 16, 1, 4, 2, 128, 64, 64, 4, 1.0, 2, None)
+                                 None, 0, 0, 0, 0, 256, 16, None, 1, 4, 2, 128, 64, 64, 4, 1.0,
+                                 2, None)
     assert rc == -1 and b"workspace" in lib.lc_last_error()
     # negative bias stride
     rc = lib.lc_paged_decode_fwd(8, 128, 128, 8, 8, 1, 1, 1, 8, 4, 4, 16, 8, 8, 128, 128, None,
-                                 8, -1, 0, 16, 0, 256, 1 << 20, 1, 4, 2, 128, 64, 64, 4, 1.0, 2,
-                                 None)
+                                 8, -1, 0, 16, 0, 256, 1 << 20, None, 1, 4, 2, 128, 64, 64, 4,
+                                 1.0, 2, None)
     assert rc == -1 and b"bias" in lib.lc_last_error()
     # unknown dtype
     rc = lib.lc_swiglu_fwd(8, 8, 8, 2, 8, 8, 8, 8, 7, None)

@@ -244,6 +244,71 @@ def test_longest_first_order_matches_split_major(cuda, dtype, P, split, masked, 
     assert_lse_close(lse_b, ref_lse)
 
 
+def _abi_decode(q, kp, vp, bt, sl, split, counters):
+    """lc_paged_decode_fwd through the C ABI with the given counters (None: the
+    static longest-first order)."""
+    from llm_cuda import _native
+    from llm_cuda.kernels import _ops
+
+    lib = _native.load()
+    B, Hq, _, D = q.shape
+    N, Hkv, P, _ = kp.shape
+    maxp = bt.shape[1]
+    max_splits = max(1, math.ceil(maxp * P / split))
+    need = lib.lc_paged_decode_workspace_bytes(B, Hq, D, max_splits)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)
+    out = torch.empty_like(q)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=q.device)
+    rc = lib.lc_paged_decode_fwd(
+        q.data_ptr(), q.stride(0), q.stride(1), kp.data_ptr(), vp.data_ptr(), kp.stride(0),
+        kp.stride(1), kp.stride(2), bt.data_ptr(), bt.stride(0), maxp, N, sl.data_ptr(),
+        out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr(), None, 0, 0, 0, 0,
+        ws.data_ptr(), ws.numel(), None if counters is None else counters.data_ptr(), B, Hq, Hkv,
+        D, P, split, max_splits, 1.0 / math.sqrt(D), _native.lc_dtype(q), _ops._stream(q.device))
+    _native.check(rc, "lc_paged_decode_fwd")
+    return out, lse
+
+
+@pytest.mark.parametrize("B,lo,hi,split", [
+    (64, 512, 8192, 3072),   # the config-2 mix: many dead slots in the grid
+    (37, 0, 6000, 2048),     # lanes past the batch, empty sequences
+    (150, 1, 6000, 2048),    # three 64-sequence chunks
+    (256, 2048, 2048, 1024),  # every slot live, equal splits: the spare pool is empty
+])
+def test_dynamic_tail_matches_static_order(cuda, B, lo, hi, split):
+    """With counters, the last quarter of the longest-first ranks is handed out
+    by a ticket in the order the workgroups start; which workgroup computes a
+    split changes none of its partials, so out and lse equal the static order
+    (NULL counters) bit for bit, call after call, and the ticket is back at zero
+    after every call (also after a smaller batch on the same counters)."""
+    from llm_cuda import _native
+
+    g = torch.Generator().manual_seed(B + split)
+    lens = torch.randint(lo, hi + 1, (B,), generator=g).tolist()
+    Hq, Hkv, D, P = 32, 8, 128, 64
+    q, kp, vp, bt, sl = _paged_case(lens, Hq, Hkv, D, P, torch.bfloat16, cuda, seed=B,
+                                    poison=False)
+    q, kp, vp, bt, sl = (t.to(cuda) for t in (q, kp, vp, bt, sl))
+    counters = torch.zeros(_native.load().lc_paged_decode_counter_count(), dtype=torch.int32,
+                           device=cuda)
+    ref_out, ref_lse = _abi_decode(q, kp, vp, bt, sl, split, None)
+    for call in range(3):
+        out, lse = _abi_decode(q, kp, vp, bt, sl, split, counters)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out), f"call {call}: output differs from the static order"
+        assert torch.equal(lse, ref_lse), f"call {call}: lse differs from the static order"
+        assert int(counters.abs().sum()) == 0, f"call {call}: ticket not returned to zero"
+    half = B // 2
+    out_h, lse_h = _abi_decode(q[:half], kp, vp, bt[:half], sl[:half], split, counters)
+    ref_h, ref_lse_h = _abi_decode(q[:half], kp, vp, bt[:half], sl[:half], split, None)
+    torch.cuda.synchronize()
+    assert torch.equal(out_h, ref_h) and torch.equal(lse_h, ref_lse_h)
+    assert int(counters.abs().sum()) == 0
+    ref, ref_l = paged_decode(q.cpu(), kp.cpu(), vp.cpu(), bt.cpu(), sl.cpu())
+    assert_close(ref_out, ref, ATOL[torch.bfloat16], f"B={B} vs oracle")
+    assert_lse_close(ref_lse, ref_l)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_paged_running_max_rescales(cuda, dtype):
     """Keys whose scores jump by ~8.7 log2 units every 64 tokens: the lazy
