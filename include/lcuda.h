@@ -134,13 +134,20 @@ LC_API int lc_rope_fwd(const void* x1, void* out1, int64_t h1, const int64_t* x1
  * softmax of equal scores does; -inf excludes a key, and a row without any
  * visible key gives o = 0, lse = -inf (the reference gives NaN there).
  * Hq % Hkv == 0. bf16/f16 run on MFMA (D in {64, 128}); other cases run a
- * generic fp32-FMA kernel (D <= 256). */
+ * generic fp32-FMA kernel (D <= 256).
+ * counters: lc_prefill_attn_counter_count() int32 values that are zero at
+ *   entry and are left zero, or NULL. With counters, the MFMA kernel hands the
+ *   lightest quarter of its row groups out to the workgroups in the order they
+ *   start (the XCDs run at different clocks); with NULL every workgroup's row
+ *   group follows from its block id. The outputs are the same either way.
+ *   Calls that may overlap (other streams) need their own counters. */
+LC_API int64_t lc_prefill_attn_counter_count(void);
 LC_API int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D,
                         const int64_t* q_strides, const int64_t* k_strides,
                         const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
                         const void* bias, const int64_t* bias_strides, int bias_dtype,
-                        float scale, int dtype, void* stream);
+                        int32_t* counters, float scale, int dtype, void* stream);
 
 /* Bytes of workspace lc_prefill_attn_bwd needs: two fp32 values per query row
  * (delta = rowsum(dO*O), and lse * log2(e)). */

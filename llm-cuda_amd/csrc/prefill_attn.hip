@@ -37,6 +37,11 @@ struct PrefillArgs {
   int64_t bs[4];
   int bias_dtype;
   int bias_vec;
+  // Dynamic tail (no bias): a ticket that is zero at entry and left zero, and
+  // the lightest dyn_light row groups of each of the dyn_units units handed
+  // out through it; dyn_light == 0: every workgroup's item from its block id.
+  int* ticket;
+  int dyn_units, dyn_light;
 };
 
 // ---------------------------------------------------------------------------
@@ -197,11 +202,53 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   // every other run of four (pf_snake) so the XCD's shader engines get equal
   // shares.
   const int nwg = gridDim.x;
+  //
+  // Dynamic tail (dyn_light > 0): the XCDs run at different clocks, so the
+  // lightest dyn_light row groups of every unit are not tied to an XCD. Block
+  // ids below S = units x (n_rbg - dyn_light) walk the heavier row groups in
+  // the order above (whole units per XCD); the others draw a rank t from the
+  // ticket as they start, t-th of the light row groups heaviest first across
+  // all units, and the extra workgroups past them (a spare pool, so that the
+  // XCDs that finish first can take more) leave at once. Every workgroup from
+  // S on draws exactly once, so the one that draws the last value returns the
+  // ticket to zero.
   const int lin = blockIdx.x;
-  int work = lin;
-  if ((nwg & 7) == 0) work = (lin & 7) * (nwg >> 3) + (lin >> 3);
-  const int unit = work / n_rbg;
-  const int rbg = n_rbg - 1 - pf_snake(work - unit * n_rbg, n_rbg);
+  int unit, rbg;
+  if (BIAS == 0 && a.dyn_light > 0) {
+    const int heavy = n_rbg - a.dyn_light;
+    const int S = a.dyn_units * heavy;
+    if (lin < S) {
+      const int w = (lin & 7) * (S >> 3) + (lin >> 3);
+      unit = w / heavy;
+      rbg = n_rbg - 1 - pf_snake(w - unit * heavy, heavy);
+    } else {
+      __shared__ int s_rank;
+      if (tid == 0) {
+        const int t = __hip_atomic_fetch_add(a.ticket, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        if (t == nwg - S - 1)
+          __hip_atomic_store(a.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_rank = t;
+      }
+      __syncthreads();
+      // (wave-uniform: kept in SGPRs, as the block-id path's values are, so
+      // the tile loop's addressing compiles as it does without the ticket)
+      const int t = __builtin_amdgcn_readfirstlane(s_rank);
+      if (t >= a.dyn_units * a.dyn_light) return;
+      unit = t % a.dyn_units;
+      rbg = a.dyn_light - 1 - t / a.dyn_units;
+    }
+  } else {
+    int work = lin;
+    if ((nwg & 7) == 0) work = (lin & 7) * (nwg >> 3) + (lin >> 3);
+    unit = work / n_rbg;
+    rbg = n_rbg - 1 - pf_snake(work - unit * n_rbg, n_rbg);
+  }
+  // Opaque from here on: the tile loop must not see which path chose them
+  // (with both paths visible its register allocation grew past the budget).
+  unit = __builtin_amdgcn_readfirstlane(unit);
+  rbg = __builtin_amdgcn_readfirstlane(rbg);
+  asm volatile("" : "+s"(unit), "+s"(rbg));
   const int kvh_hg = unit % (a.Hkv * n_hg);
   const int b = unit / (a.Hkv * n_hg);
   const int kvh = kvh_hg / n_hg;
@@ -653,7 +700,22 @@ int launch_mfma(const PrefillArgs& a, hipStream_t st) {
   const int64_t nwg = (int64_t)n_rbg * a.Hkv * (a.G / hw) * a.B;
   LC_REQUIRE(nwg < (1LL << 31), "lc_prefill_attn_fwd: grid too large");
   dim3 grid(static_cast<unsigned>(nwg));
-  if (a.bias == nullptr)
+  // Dynamic tail: with a ticket, no bias, whole units per XCD (units a
+  // multiple of 8), >= 8 row groups per unit and more than two rounds of
+  // workgroups (two per CU). Measured at config 3 against the static order in
+  // one process (two boxes): 0.5165 vs 0.5213 ms and 0.5073 vs 0.5114 ms with
+  // a light quarter and a spare pool of nwg / 16; a third, a fifth, or spare
+  // pools of nwg / 8 and nwg / 32 were no better.
+  const int units = static_cast<int>(nwg / n_rbg);
+  if (a.ticket != nullptr && a.bias == nullptr && units % 8 == 0 && n_rbg >= 8 &&
+      nwg > 2LL * lc_cu_count()) {
+    PrefillArgs d = a;
+    d.dyn_units = units;
+    d.dyn_light = n_rbg / 4;
+    const int64_t spare = nwg / 16;
+    LC_REQUIRE(nwg + spare < (1LL << 31), "lc_prefill_attn_fwd: grid too large");
+    launch_mfma_bias<T, 0>(d, dim3(static_cast<unsigned>(nwg + spare)), hw, n_rbg, st);
+  } else if (a.bias == nullptr)
     launch_mfma_bias<T, 0>(a, grid, hw, n_rbg, st);
   else if (a.bias_dtype == LC_DTYPE_F32)
     launch_mfma_bias<T, 2>(a, grid, hw, n_rbg, st);
@@ -680,14 +742,17 @@ int launch_generic(const PrefillArgs& a, hipStream_t st) {
 
 extern "C" {
 
+int64_t lc_prefill_attn_counter_count(void) { return 64; }
+
 int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D,
                         const int64_t* q_strides, const int64_t* k_strides,
                         const int64_t* v_strides, const int64_t* o_strides, int64_t q_offset,
                         const void* bias, const int64_t* bias_strides, int bias_dtype,
-                        float scale, int dtype, void* stream) {
+                        int32_t* counters, float scale, int dtype, void* stream) {
   LC_REQUIRE(q_strides && k_strides && v_strides && o_strides,
              "lc_prefill_attn_fwd: null stride array");
+  LC_REQUIRE(lc_aligned(counters, 4), "lc_prefill_attn_fwd: counters not 4-byte aligned");
   LC_REQUIRE(B >= 0 && B < 65536 && Sq >= 0 && Skv >= 0, "lc_prefill_attn_fwd: bad shape");
   // Pointers of empty tensors may be null.
   LC_REQUIRE((q && o) || B * Sq == 0, "lc_prefill_attn_fwd: null q or o");
@@ -734,6 +799,7 @@ int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, fl
   a.scale_log2 = scale * kLog2e;
   a.bias = Skv > 0 ? bias : nullptr;
   a.bias_dtype = bias_dtype;
+  a.ticket = counters;
   if (bias != nullptr)
     for (int i = 0; i < 4; ++i) a.bs[i] = bias_strides[i];
   hipStream_t st = lc_stream(stream);

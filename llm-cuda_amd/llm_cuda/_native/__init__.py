@@ -53,10 +53,11 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_i64, _c_i64p, _c_i64p, _c_p, _c_p, _c_i64, _c_i64p, _c_i64p, _c_p, _c_p,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_int, _c_p],
     ),
+    "lc_prefill_attn_counter_count": (_c_i64, []),
     "lc_prefill_attn_fwd": (
         ctypes.c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p,
-         _c_i64p, _c_i64p, _c_i64p, _c_i64, _c_p, _c_i64p, ctypes.c_int, ctypes.c_float,
+         _c_i64p, _c_i64p, _c_i64p, _c_i64, _c_p, _c_i64p, ctypes.c_int, _c_p, ctypes.c_float,
          ctypes.c_int, _c_p],
     ),
     "lc_prefill_attn_bwd_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),

@@ -381,6 +381,10 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offse
     out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=dev)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=dev) if return_lse else None
     lib = nat.load()
+    # The ticket of the kernel's dynamic tail (zero-on-exit); a capture before
+    # any eager call runs the static order (no counters).
+    counters = _zeroed_counters("prefill", dev, lib.lc_prefill_attn_counter_count(),
+                                optional=True)
     with _DeviceGuard(dev):
         rc = lib.lc_prefill_attn_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
@@ -388,7 +392,9 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_offse
             _i64arr(q.stride()), _i64arr(k.stride()), _i64arr(v.stride()), _i64arr(out.stride()),
             int(q_offset), None if bias is None else bias.data_ptr(),
             None if bias is None else _i64arr(bias.stride()),
-            0 if bias is None else nat.lc_dtype(bias), float(scale), nat.lc_dtype(q), _stream(dev))
+            0 if bias is None else nat.lc_dtype(bias),
+            None if counters is None else counters.data_ptr(), float(scale), nat.lc_dtype(q),
+            _stream(dev))
     nat.check(rc, "lc_prefill_attn_fwd")
     return (out, lse) if return_lse else out
 
@@ -506,7 +512,8 @@ _RETIRED_COUNTERS: list = []
 def _zeroed_counters(kind: str, dev: torch.device, n: int, optional: bool = False):
     """Zeroed int32 counters for the kernels that take them (`kind`:
     "decode_linear" ticket counters, "lm_head" argmax keys and ticket,
-    "paged_decode" the ticket of the longest-first order's dynamic tail). Each
+    "paged_decode" the ticket of the longest-first order's dynamic tail,
+    "prefill" the ticket of the prefill kernel's dynamic tail). Each
     call leaves its counters at zero, so calls that follow one another on a
     stream can share a buffer; calls on different streams (which may overlap)
     must not. Eager calls get one buffer per (kind, device, stream). Calls

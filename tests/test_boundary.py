@@ -88,14 +88,14 @@ def test_invalid_arguments_rejected_before_launch():
     assert rc == -1 and b"null" in lib.lc_last_error()
     # Hq not a multiple of Hkv
     rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 5, 3, 4, 4, 16, st, st, st, st, 0, None,
-                                 None, 0, 1.0, 2, None)
+                                 None, 0, None, 1.0, 2, None)
     assert rc == -1 and b"multiple" in lib.lc_last_error()
     # a bias without strides, or of a third dtype
     rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 4, 2, 4, 4, 16, st, st, st, st, 0, 8,
-                                 None, 0, 1.0, 2, None)
+                                 None, 0, None, 1.0, 2, None)
     assert rc == -1 and b"bias_strides" in lib.lc_last_error()
     rc = lib.lc_prefill_attn_fwd(8, 8, 8, 8, None, 1, 4, 2, 4, 4, 16, st, st, st, st, 0, 8,
-                                 st, 1, 1.0, 2, None)
+                                 st, 1, None, 1.0, 2, None)
     assert rc == -1 and b"bias dtype" in lib.lc_last_error()
     # odd head_dim for RoPE
     rc = lib.lc_rope_fwd(8, 8, 1, st, st, None, None, 0, None, None, 8, 8, 15, 15, 1, 1, 15, 2,
@@ -304,13 +304,13 @@ def test_empty_extents_accept_null_pointers():
     lib = _native.load()
     st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
     rc = lib.lc_prefill_attn_fwd(None, 8, 8, None, None, 1, 4, 2, 0, 16, 64, st, st, st, st, 0,
-                                 None, None, 0, 1.0, 2, None)
+                                 None, None, 0, None, 1.0, 2, None)
     assert rc == 0
     rc = lib.lc_prefill_attn_fwd(None, 8, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, None,
-                                 None, 0, 1.0, 2, None)
+                                 None, 0, None, 1.0, 2, None)
     assert rc == -1 and b"null q" in lib.lc_last_error()
     rc = lib.lc_prefill_attn_fwd(8, None, 8, 8, None, 1, 4, 2, 3, 16, 64, st, st, st, st, 0, None,
-                                 None, 0, 1.0, 2, None)
+                                 None, 0, None, 1.0, 2, None)
     assert rc == -1 and b"null k" in lib.lc_last_error()
 
 
