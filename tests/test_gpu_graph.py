@@ -66,3 +66,55 @@ def test_decode_step_graph_replays_match_eager(cuda):
             assert torch.isfinite(junk)
             assert torch.equal(g_ids, eager_ids), f"replay {rep}: ids differ"
             assert torch.equal(g_best, eager_best), f"replay {rep}: winning logits differ"
+
+
+@pytest.mark.parametrize("eager_first", [True, False])
+def test_ragged_decode_graph_replays_with_ticket(cuda, eager_first):
+    """A ragged paged decode whose split workgroups take several rounds of the
+    CUs (the longest-first order with its ticket-handed tail) captured in a HIP
+    graph: with an eager call first the capture uses the per-device graph
+    counters, without one it runs the static order. Every replay, with eager
+    calls in between, reproduces the eager output bit for bit, and the graph
+    counters are back at zero after each replay."""
+    import math
+
+    from llm_cuda.kernels import _ops
+    from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
+
+    _ops._COUNTERS.pop(("paged_decode", "cuda", cuda.index, "graphs"), None)
+    g = torch.Generator().manual_seed(7)
+    B, Hq, Hkv, D, P = 64, 32, 8, 128, 64
+    lens = torch.randint(512, 8193, (B,), generator=g)
+    maxp = math.ceil(int(lens.max()) / P)
+    N = B * maxp
+    bt = torch.randperm(N, generator=g).to(torch.int32).view(B, maxp).to(cuda)
+    kp = torch.randn(N, Hkv, P, D, generator=g).to(torch.bfloat16).to(cuda)
+    vp = torch.randn(N, Hkv, P, D, generator=g).to(torch.bfloat16).to(cuda)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16).to(cuda)
+    sl = lens.to(torch.int32).to(cuda)
+
+    def run():
+        return paged_decode_attention(q, kp, vp, bt, sl, return_lse=True)
+
+    ref_out, ref_lse = run()
+    ref_out, ref_lse = ref_out.clone(), ref_lse.clone()
+    if not eager_first:
+        _ops._COUNTERS.pop(("paged_decode", "cuda", cuda.index, "graphs"), None)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            g_out, g_lse = run()
+    torch.cuda.current_stream().wait_stream(side)
+    key = ("paged_decode", "cuda", cuda.index, "graphs")
+    assert (key in _ops._COUNTERS) == eager_first
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, ref_out), f"replay {rep}: output differs from eager"
+        assert torch.equal(g_lse, ref_lse), f"replay {rep}: lse differs from eager"
+        if eager_first:
+            assert int(_ops._COUNTERS[key].abs().sum()) == 0
+        out, lse = run()  # eager work between replays
+        assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse)
