@@ -183,6 +183,7 @@ def _abi_prefill(q, k, v, q_offset, counters):
     (4, 32, 8, 1024, 3072, 128),   # cached prefix (q_offset 2048)
     (1, 64, 8, 2048, 2048, 128),   # 8 q heads per kv head: two head groups per kv head
     (2, 16, 8, 4096, 4096, 64),    # two rows of 32 per head group (G = 2)
+    (2, 32, 8, 2000, 2000, 128),   # 63 row groups, the last one partial
 ])
 def test_dynamic_tail_matches_static_order(cuda, B, Hq, Hkv, Sq, Skv, D):
     """With counters, the lightest quarter of the MFMA kernel's row groups is
