@@ -160,6 +160,8 @@ constexpr int kPfWaves = 4;
 constexpr int kPfRows = 32;     // query rows per wave
 constexpr int kPfKeys = 64;     // keys per tile
 constexpr float kPfRescaleLog2 = 8.0f;
+// int32 counters lc_prefill_attn_fwd takes: the dynamic tail's ticket, padded to 256 bytes.
+constexpr int kPrefillCounterInts = 64;
 
 // With an additive bias (BIAS != 0) the kernel runs one wave per SIMD: the
 // bias tile held one iteration ahead does not fit the two-wave register
@@ -742,7 +744,7 @@ int launch_generic(const PrefillArgs& a, hipStream_t st) {
 
 extern "C" {
 
-int64_t lc_prefill_attn_counter_count(void) { return 64; }
+int64_t lc_prefill_attn_counter_count(void) { return kPrefillCounterInts; }
 
 int lc_prefill_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D,
