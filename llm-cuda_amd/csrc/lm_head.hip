@@ -11,7 +11,8 @@
 //   * lm_head_argmax_mfma_kernel (bf16/f16, K % 128 == 0, up to 32 hidden rows
 //     per launch): one workgroup per CU, each owning a contiguous range of
 //     vocab rows (V / grid, balanced to one row), which it walks in blocks of
-//     64 rows. Weight rows stream through LDS in 256-column tiles (buffer-to-
+//     64 rows; with the counters, k whole blocks each and then single blocks
+//     drawn from a pool by a ticket, so the faster XCDs take more of them. Weight rows stream through LDS in 256-column tiles (buffer-to-
 //     LDS DMA, 512-byte runs per row, a three-stage ring with two tiles in
 //     flight) together with the matching 256 columns of the hidden rows; the
 //     ring runs on across block boundaries, so a block's start and finish
@@ -95,6 +96,10 @@ struct LhArgs {
   // Packed best keys [kLhBatch] followed by the ticket (zero at entry, left
   // zero), or null: partials for the reduce kernel.
   unsigned long long* keys;
+  // Block pool (with the counters): the vocab blocks from pool_begin on are
+  // handed out by a ticket; null: every workgroup owns a contiguous range.
+  int* pool_ticket;
+  int pool_begin, pool_blocks;
   int64_t* ids;
   float* max_out;
   int64_t hs, ws;  // row strides (elements)
@@ -126,6 +131,7 @@ __device__ __forceinline__ int lh_unpack_index(unsigned long long key) {
   return static_cast<int>(~static_cast<uint32_t>(key));
 }
 constexpr int kLhCounterInts = (kLhBatch * 8 + 16) / 4;  // keys + ticket (+ padding)
+constexpr int kLhPoolTicket = kLhBatch * 2 + 2;  // int index of the block pool's ticket
 
 template <typename T>
 __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhArgs a) {
@@ -159,11 +165,14 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   const int kh = wave_s / kLhRowWaves;  // column half of each tile
   // This workgroup's vocab rows [r_begin, r_end), in blocks of kLhRows.
   const int nwg = gridDim.x;
-  const int r_begin = static_cast<int>((int64_t)a.V * blockIdx.x / nwg);
-  const int r_end = static_cast<int>((int64_t)a.V * (blockIdx.x + 1) / nwg);
-  const int nb = (r_end - r_begin + kLhRows - 1) / kLhRows;
+  // With a block pool, the first range is pool_begin / nwg whole blocks and
+  // later ranges are single blocks drawn from the pool.
+  const int sb = a.pool_ticket != nullptr ? a.pool_begin / kLhRows / nwg : 0;
+  int rb_next = a.pool_ticket != nullptr ? static_cast<int>(blockIdx.x) * sb * kLhRows
+                                         : static_cast<int>((int64_t)a.V * blockIdx.x / nwg);
+  int re_next = a.pool_ticket != nullptr ? min(a.V, rb_next + sb * kLhRows)
+                                         : static_cast<int>((int64_t)a.V * (blockIdx.x + 1) / nwg);
   const int n_tiles = (a.K + kLhKc - 1) / kLhKc;
-  const int G = nb * n_tiles;  // tiles of the whole range
   const T* wbase = static_cast<const T*>(a.weight);
   // Rows past the range (and hidden rows past B) are out of the descriptors'
   // range and land in LDS as zeros.
@@ -201,7 +210,7 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   const int wrow0 = rw * 32 * ROW_B;
 
   // Tile ft of block fb into ring stage st.
-  auto fetch = [&](int fb, int ft, int st) __attribute__((always_inline)) {
+  auto fetch = [&](int fb, int ft, int st, int r_begin, int r_end) __attribute__((always_inline)) {
     const int row0 = r_begin + fb * kLhRows;
     const int valid = min(kLhRows, r_end - row0);
     const int wbytes = static_cast<int>(((int64_t)(valid - 1) * a.ws + a.K) * sizeof(T));
@@ -232,7 +241,7 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   // as a packed key (lh_pack; 0 = none yet). Branch-free.
   float keep[16];
   unsigned long long best = 0;
-  auto block_epilogue = [&](int blk) __attribute__((always_inline)) {
+  auto block_epilogue = [&](int blk, int r_begin, int r_end) __attribute__((always_inline)) {
     if (kh == 0) {
       const int row0 = r_begin + blk * kLhRows;
       const int valid = min(kLhRows, r_end - row0);
@@ -273,40 +282,70 @@ __global__ __launch_bounds__(64 * kLhWaves) void lm_head_argmax_mfma_kernel(LhAr
   // tile's second half is past K, and its waves skip that tile's products.
   const bool skip_last = kh == 1 && (a.K % kLhKc) != 0;
   constexpr int kNi = NIW_W + NIW_H;  // DMA instructions per wave per tile
-  if (G > 0) fetch(0, 0, 0);
-  if (G > 1) fetch(n_tiles > 1 ? 0 : 1, n_tiles > 1 ? 1 : 0, 1);
-  int fb = n_tiles > 2 ? 0 : (n_tiles == 2 ? 1 : 2);  // tile 2 of the range
-  int ft = n_tiles > 2 ? 2 : 0;
-  int st = 0;
-  int g = 0;
-  for (int blk = 0; blk < nb; ++blk) {
-    for (int t = 0; t < n_tiles; ++t, ++g) {
-      if (g + 1 < G)
-        __builtin_amdgcn_s_waitcnt(lh_waitcnt(kNi, 0));
-      else
-        __builtin_amdgcn_s_waitcnt(lh_waitcnt(0, 0));
-      lc_compiler_fence();
-      __builtin_amdgcn_s_barrier();
-      lc_compiler_fence();
-      if (t == 0 && blk > 0) block_epilogue(blk - 1);
-      if (g + 2 < G) {
-        fetch(fb, ft, st == 0 ? 2 : st - 1);
-        if (++ft == n_tiles) {
-          ft = 0;
-          ++fb;
+  // Ranges of rows, one after another: the workgroup's own range, then (with
+  // a block pool) one block at a time drawn from the pool until it is empty.
+  // Every workgroup draws once per pool block it takes plus one final draw,
+  // so the draws number pool_blocks + nwg and the last one returns the ticket
+  // to zero. The running best carries over from range to range.
+  int last_nb = 0;
+  for (;;) {
+    const int r_begin = __builtin_amdgcn_readfirstlane(rb_next);
+    const int r_end = __builtin_amdgcn_readfirstlane(re_next);
+    const int nb = (r_end - r_begin + kLhRows - 1) / kLhRows;
+    const int G = nb * n_tiles;  // tiles of the range
+    if (G > 0) fetch(0, 0, 0, r_begin, r_end);
+    if (G > 1) fetch(n_tiles > 1 ? 0 : 1, n_tiles > 1 ? 1 : 0, 1, r_begin, r_end);
+    int fb = n_tiles > 2 ? 0 : (n_tiles == 2 ? 1 : 2);  // tile 2 of the range
+    int ft = n_tiles > 2 ? 2 : 0;
+    int st = 0;
+    int g = 0;
+    for (int blk = 0; blk < nb; ++blk) {
+      for (int t = 0; t < n_tiles; ++t, ++g) {
+        if (g + 1 < G)
+          __builtin_amdgcn_s_waitcnt(lh_waitcnt(kNi, 0));
+        else
+          __builtin_amdgcn_s_waitcnt(lh_waitcnt(0, 0));
+        lc_compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        lc_compiler_fence();
+        if (t == 0 && blk > 0) block_epilogue(blk - 1, r_begin, r_end);
+        if (g + 2 < G) {
+          fetch(fb, ft, st == 0 ? 2 : st - 1, r_begin, r_end);
+          if (++ft == n_tiles) {
+            ft = 0;
+            ++fb;
+          }
         }
+        if (!(skip_last && t == n_tiles - 1)) compute(st);
+        st = st == 2 ? 0 : st + 1;
       }
-      if (!(skip_last && t == n_tiles - 1)) compute(st);
-      st = st == 2 ? 0 : st + 1;
+      block_end(blk);
     }
-    block_end(blk);
+    __syncthreads();  // the last block's second-half sums are in LDS
+    if (nb > 0) block_epilogue(nb - 1, r_begin, r_end);
+    last_nb = nb;
+    if (a.pool_ticket == nullptr) break;
+    // The draw goes through the exchange buffer this range's last block left
+    // free (the next range writes it only after its first block's barriers).
+    int* s_draw = reinterpret_cast<int*>(xch[nb & 1]) + (XCH - 1);
+    if (tid == 0) {
+      const int t = __hip_atomic_fetch_add(a.pool_ticket, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      if (t == a.pool_blocks + nwg - 1)
+        __hip_atomic_store(a.pool_ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *s_draw = t;
+    }
+    __syncthreads();
+    const int t = __builtin_amdgcn_readfirstlane(*s_draw);
+    __syncthreads();
+    if (t >= a.pool_blocks) break;
+    rb_next = a.pool_begin + t * kLhRows;
+    re_next = min(a.V, rb_next + kLhRows);
   }
-  __syncthreads();  // the last block's second-half sums are in LDS
-  if (nb > 0) block_epilogue(nb - 1);
   // Workgroup best per batch row: the two lane halves, then the row groups
-  // through the exchange buffer the last block did not use (xch[nb & 1], free
-  // since the last barrier).
-  unsigned long long* red = reinterpret_cast<unsigned long long*>(xch[nb & 1]);
+  // through the exchange buffer the last block did not use (xch[last_nb & 1],
+  // free since the last barrier).
+  unsigned long long* red = reinterpret_cast<unsigned long long*>(xch[last_nb & 1]);
   if (kh == 0) {
     const uint32_t lo = static_cast<uint32_t>(best), hi = static_cast<uint32_t>(best >> 32);
     best = lh_max_key(best, (static_cast<unsigned long long>(__shfl_xor(hi, 32, 64)) << 32) |
@@ -448,6 +487,22 @@ int run_lm_head_mfma(LhArgs a, int64_t* ids, float* max_out, hipStream_t st) {
   const T* hidden = static_cast<const T*>(a.hidden);
   const int B = a.B;
   a.pstride = kLhBatch;
+  // Block pool (fused selection only, it needs the counters): each workgroup
+  // first takes k whole 64-row blocks, k leaving at least half a block per
+  // workgroup to the pool; the rest go to whichever workgroups finish first
+  // (the XCDs stream at different rates). At the Llama-3-8B vocab (2004
+  // blocks, 256 workgroups) k = 7: 152.8-153.0 us against 164.7-165.0 us for
+  // contiguous ranges in an A/B on one box (k = 6 153-154, 5 157-158, 4 161).
+  a.pool_ticket = nullptr;
+  {
+    const int nblk = static_cast<int>((a.V + kLhRows - 1) / kLhRows);
+    const int k = (nblk - n_wg / 2) / n_wg;
+    if (a.keys != nullptr && k >= 1 && k * n_wg < nblk) {
+      a.pool_ticket = reinterpret_cast<int*>(a.keys) + kLhPoolTicket;
+      a.pool_begin = k * n_wg * kLhRows;
+      a.pool_blocks = nblk - k * n_wg;
+    }
+  }
   for (int b0 = 0; b0 < B; b0 += kLhBatch) {
     a.hidden = hidden + (int64_t)b0 * a.hs;
     a.B = min(kLhBatch, B - b0);

@@ -131,11 +131,14 @@ def _abi_call(hidden, weight, counters):
 
 
 @pytest.mark.parametrize("B,K,V", [(1, 128, 10), (32, 4096, 20000), (33, 512, 3000),
-                                   (7, 256, 16385), (4, 1024, 64)])
+                                   (7, 256, 16385), (4, 1024, 64),
+                                   (32, 512, 60000),    # block pool: 3 blocks each, 170 drawn
+                                   (5, 256, 128256)])   # the 8B vocab: 7 blocks each, 212 drawn
 def test_lm_head_fused_select_matches_reduce_launch(cuda, B, K, V):
     """The MFMA path's in-kernel selection (packed keys + ticket, with a
-    counters buffer) gives the ids and logits of its partials + reduce-launch
-    form, call after call, and leaves the counters at zero. Rows of zeros
+    counters buffer; from 1.5 blocks per workgroup on, blocks also drawn from
+    a pool) gives the ids and logits of its partials + reduce-launch form
+    (contiguous ranges), call after call, and leaves the counters at zero. Rows of zeros
     (every logit +-0: the smallest index wins), copied winners (ties) and a
     NaN row are included."""
     from llm_cuda import _native
