@@ -561,6 +561,12 @@ def torch_projections():
         _NATIVE_PROJECTIONS[0] = prev
 
 
+def native_projections() -> bool:
+    """False inside torch_projections(): the decode-step projections are torch
+    matmuls there."""
+    return _NATIVE_PROJECTIONS[0]
+
+
 def decode_linear_applies(x: torch.Tensor, weight: torch.Tensor, swiglu: bool = False) -> bool:
     """True where decode_linear takes the call: bf16/f16 on the GPU, 1-32 rows,
     K % 128 == 0, an output width N % 4 == 0, aligned rows, no autograd graph

@@ -54,3 +54,27 @@ def test_usable_only_without_autograd_recording():
     for lin in (a, b, c):
         lin.weight.requires_grad_(False)
     assert FusedLinearWeights.usable(a, b, c)
+
+
+def test_column_layout_is_the_transpose_and_aliases_the_parameters():
+    """weight(columns=True): W^T stored contiguously, [K, sum N], each
+    parameter a transposed column block of it; in-place updates reach it and
+    asking for the other layout rebuilds with the same values."""
+    a, b, c = _linears()
+    ref = torch.cat([a.weight, b.weight, c.weight]).detach().clone()
+    f = FusedLinearWeights(a, b, c)
+    wt = f.weight(columns=True)
+    assert wt.shape == (16, 16) and wt.is_contiguous() and torch.equal(wt, ref.t())
+    assert a.weight.shape == (8, 16) and a.weight.stride() == (1, 16)
+    assert b.weight.data_ptr() == wt.data_ptr() + 8 * 4
+    assert torch.equal(torch.cat([a.weight, b.weight, c.weight]), ref)
+    assert f.weight(columns=True) is wt  # cached while the aliasing holds
+    x = torch.randn(3, 16)
+    assert torch.allclose(x @ wt, torch.cat([a(x), b(x), c(x)], -1), atol=1e-6)
+    with torch.no_grad():
+        c.weight.copy_(torch.full_like(c.weight, 3.0))
+    assert f.weight(columns=True) is wt and torch.equal(wt[:, 12:], torch.full((16, 4), 3.0))
+    w = f.weight()  # back to rows: one rebuild, same values
+    assert w.is_contiguous() and w.shape == (16, 16) and torch.equal(w[12:], wt[:, 12:].t())
+    assert torch.equal(w[:12], ref[:12]) and a.weight.data_ptr() == w.data_ptr()
+    assert f.weight(columns=True) is not wt

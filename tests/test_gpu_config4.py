@@ -237,13 +237,28 @@ def _eager_step(model, cache, ids):
     return hidden, nxt, best
 
 
-def test_config4_two_layers_every_block_matches_oracle(cuda, monkeypatch):
+@pytest.mark.parametrize("projections", ["native", "torch"])
+def test_config4_two_layers_every_block_matches_oracle(cuda, monkeypatch, projections):
     """Two full-width layers of the config-4 step (full vocabulary), every block
-    of both layers and the greedy ids against the oracle."""
+    of both layers and the greedy ids against the oracle; with the projections
+    on the native kernel, and as torch matmuls (BASELINE config 4 as stated:
+    the MLP's [gate; up] weight then kept transposed, the parameters views of
+    it)."""
+    import contextlib
+
+    from llm_cuda.kernels import _ops
+
     cfg, model, cache, ids = _build(cuda, layers=2)
     cap = _Capture(model, monkeypatch)
-    hidden, nxt, best = _eager_step(model, cache, ids)
+    ctx = _ops.torch_projections() if projections == "torch" else contextlib.nullcontext()
+    with ctx:
+        hidden, nxt, best = _eager_step(model, cache, ids)
     cap.remove()
+    if projections == "torch":
+        mlp = model.model.layers[0].mlp
+        wt = mlp._gate_up.buf
+        assert mlp._gate_up.columns and wt.shape == (cfg.hidden_size, 2 * cfg.intermediate_size)
+        assert mlp.up_proj.weight.data_ptr() == wt.data_ptr() + cfg.intermediate_size * 2
     assert len(cap.dec) == 2 and len(cap.attn_in) == 2 and len(cap.mlp_out) == 2
     # 32 sequences x 8 kv heads fill the 256 CUs once: the fused step runs
     assert cap.fused == 2 or torch.cuda.get_device_properties(0).multi_processor_count != 256
