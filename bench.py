@@ -589,10 +589,10 @@ def run_model(args, projections=None, cpu_cache=None):
         f"{weights / 1e9:.2f} GB + KV {kv / 1e9:.2f} GB per step -> {gbs:.0f} GB/s "
         f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
     if projections == "torch":
-        proj_desc = ("torch F.linear (hipBLASLt), as BASELINE config 4 states: one GEMM for "
-                     "q/k/v and one for gate/up (concatenated weights), o and down; SwiGLU, "
-                     "RoPE + KV append + decode attention, add + RMSNorm and lm_head + argmax "
-                     "on the HIP kernels")
+        proj_desc = ("torch matmuls (hipBLASLt), as BASELINE config 4 states: one GEMM for "
+                     "q/k/v and one for gate/up (concatenated weights, gate/up stored "
+                     "transposed), o and down; SwiGLU, RoPE + KV append + decode attention, "
+                     "add + RMSNorm and lm_head + argmax on the HIP kernels")
         profile = "model8b_decode_step_torch_proj"
     else:
         proj_desc = "native lc_decode_linear: fused q/k/v, o, gate/up + SwiGLU, down"
