@@ -1,0 +1,129 @@
+"""Seeded random shapes for the three data-dependent kernels, against the oracle.
+
+Each case draws its shape from a numpy generator seeded by the case number, so
+the set is fixed and every failure names a reproducible case (the pytest id
+carries the shape). Shapes stay small enough for the CPU oracle; they cover
+what the hand-picked cases elsewhere fix only at chosen points: odd batch
+sizes, group sizes 1-16, head_dims 64-256, page sizes 16-128 (and 48, not a
+power of two), empty and one-token sequences, split sizes chosen by the
+library or forced, cached-prefix offsets, vocabularies that are not tile
+multiples.
+
+Decode: out within the dtype's atol and lse within 1e-3 relative of
+oracle.decode.paged_decode; pools poisoned with NaN outside the sequences'
+slots (a stray read shows up as NaN); a second call equal bit for bit.
+Prefill: oracle.attention.causal_attention with the same q_offset.
+lm_head + argmax: the ids rule of tests/test_gpu_lm_head.py (one ulp of slack
+at a rounding boundary, at most one such row).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import ATOL, assert_close, assert_lse_close
+from oracle.attention import causal_attention
+from oracle.decode import paged_decode
+from test_gpu_decode import _paged_case
+from test_gpu_lm_head import _check as _check_lm_head
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode_case(i):
+    r = np.random.default_rng(1000 + i)
+    dtype = torch.float16 if r.random() < 0.3 else torch.bfloat16
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    G = int(r.choice([1, 2, 3, 4, 8, 16]))
+    D = int(r.choice([64, 96, 128, 128, 256]))
+    P = int(r.choice([16, 32, 48, 64, 64, 128]))
+    B = int(r.integers(1, 81))
+    lmax = int(r.choice([64, 700, 3000, 6000]))
+    # bound the pools (and the oracle's work): tokens x Hkv x D <= 2^25
+    lmax = max(1, min(lmax, (1 << 25) // (B * Hkv * D)))
+    lens = r.integers(0, lmax + 1, B)
+    lens[r.random(B) < 0.1] = 0
+    if B > 2:
+        lens[int(r.integers(0, B))] = 1
+    split = None if r.random() < 0.5 else int(r.choice([64, 256, 512, 1024, 2048, 3072]))
+    return dict(lens=[int(x) for x in lens], Hq=Hkv * G, Hkv=Hkv, D=D, P=P, dtype=dtype,
+                split=split)
+
+
+def _prefill_case(i):
+    r = np.random.default_rng(2000 + i)
+    dtype = torch.float16 if r.random() < 0.3 else torch.bfloat16
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    G = int(r.choice([1, 2, 4, 8]))
+    D = int(r.choice([64, 128, 128]))
+    B = int(r.integers(1, 4))
+    Sq = int(r.integers(1, 600))
+    off = 0 if r.random() < 0.5 else int(r.integers(1, 300))
+    # bound the oracle's work: B x Hq x Sq x Skv x D <= 2^31
+    while B * Hkv * G * Sq * (Sq + off) * D > (1 << 31) and Sq > 1:
+        Sq //= 2
+    return dict(B=B, Hq=Hkv * G, Hkv=Hkv, Sq=Sq, off=off, D=D, dtype=dtype)
+
+
+def _lm_head_case(i):
+    r = np.random.default_rng(3000 + i)
+    dtype = torch.float16 if r.random() < 0.3 else torch.bfloat16
+    B = int(r.integers(1, 71))
+    K = int(r.choice([128, 256, 384, 512, 1024, 4096]))
+    V = int(r.integers(2, 30001))
+    V = max(2, min(V, (1 << 25) // K))
+    return dict(B=B, K=K, V=V, dtype=dtype)
+
+
+def _id(case):
+    return "-".join(f"{k}{v}" if k != "lens" else f"B{len(v)}max{max(v)}"
+                    for k, v in case.items() if k != "dtype") + \
+        ("-f16" if case["dtype"] == torch.float16 else "-bf16")
+
+
+DECODE = [_decode_case(i) for i in range(24)]
+PREFILL = [_prefill_case(i) for i in range(16)]
+LM_HEAD = [_lm_head_case(i) for i in range(16)]
+
+
+@pytest.mark.parametrize("case", DECODE, ids=[_id(c) for c in DECODE])
+def test_fuzz_paged_decode(cuda, case):
+    from llm_cuda.kernels.triton.decode_attention import paged_decode_attention
+
+    c = case
+    q, kp, vp, bt, sl = _paged_case(c["lens"], c["Hq"], c["Hkv"], c["D"], c["P"], c["dtype"],
+                                    cuda, seed=len(c["lens"]), poison=True)
+    kw = {} if c["split"] is None else {"split_tokens": c["split"]}
+    dev = [t.to(cuda) for t in (q, kp, vp, bt, sl)]
+    out, lse = paged_decode_attention(*dev, return_lse=True, **kw)
+    out2, lse2 = paged_decode_attention(*dev, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2) and torch.equal(lse, lse2), "second call differs"
+    ref, ref_lse = paged_decode(q, kp, vp, bt, sl)
+    assert_close(out, ref, ATOL[c["dtype"]], f"decode {_id(c)}")
+    assert_lse_close(lse, ref_lse, f"decode lse {_id(c)}")
+
+
+@pytest.mark.parametrize("case", PREFILL, ids=[_id(c) for c in PREFILL])
+def test_fuzz_prefill(cuda, case):
+    from llm_cuda.kernels.triton.attention import triton_fused_causal_attention
+
+    c = case
+    g = torch.Generator().manual_seed(c["Sq"] * 31 + c["off"])
+    Skv = c["Sq"] + c["off"]
+    q = torch.randn(c["B"], c["Hq"], c["Sq"], c["D"], generator=g).to(c["dtype"])
+    k = torch.randn(c["B"], c["Hkv"], Skv, c["D"], generator=g).to(c["dtype"])
+    v = torch.randn(c["B"], c["Hkv"], Skv, c["D"], generator=g).to(c["dtype"])
+    out, lse = triton_fused_causal_attention(q.to(cuda), k.to(cuda), v.to(cuda),
+                                             return_lse=True, q_offset=c["off"])
+    ref, ref_lse = causal_attention(q, k, v, q_offset=c["off"])
+    assert_close(out, ref, ATOL[c["dtype"]], f"prefill {_id(c)}")
+    assert_lse_close(lse, ref_lse, f"prefill lse {_id(c)}")
+
+
+@pytest.mark.parametrize("case", LM_HEAD, ids=[_id(c) for c in LM_HEAD])
+def test_fuzz_lm_head_argmax(cuda, case):
+    c = case
+    g = torch.Generator().manual_seed(c["V"] + c["K"])
+    hidden = torch.randn(c["B"], c["K"], generator=g).to(c["dtype"]).to(cuda)
+    weight = (torch.randn(c["V"], c["K"], generator=g) * 0.02).to(c["dtype"]).to(cuda)
+    _check_lm_head(hidden, weight, max_mismatch=1)
