@@ -1,10 +1,10 @@
-"""Seeded random shapes for the three data-dependent kernels, against the oracle.
+"""Seeded random shapes for the attention, decode-step and lm_head kernels, against the oracle.
 
 Each case draws its shape from a numpy generator seeded by the case number, so
 the set is fixed and every failure names a reproducible case (the pytest id
 carries the shape). Shapes stay small enough for the CPU oracle; they cover
 what the hand-picked cases elsewhere fix only at chosen points: odd batch
-sizes, group sizes 1-16, head_dims 64-256, page sizes 16-128 (and 48, not a
+sizes, group sizes 1-20, head_dims 64-256, page sizes 16-128 (and 48, not a
 power of two), empty and one-token sequences, split sizes chosen by the
 library or forced, cached-prefix offsets, vocabularies that are not tile
 multiples.
@@ -12,7 +12,12 @@ multiples.
 Decode: out within the dtype's atol and lse within 1e-3 relative of
 oracle.decode.paged_decode; pools poisoned with NaN outside the sequences'
 slots (a stray read shows up as NaN); a second call equal bit for bit.
-Prefill: oracle.attention.causal_attention with the same q_offset.
+Fused decode step: pools and lengths bit-identical to RoPE + append, out and
+lse against the oracle's decode over the advanced lengths (the rule of
+tests/test_gpu_decode_step.py), positions past the capacity included.
+Prefill: oracle.attention.causal_attention with the same q_offset; backward:
+oracle.attention.causal_attention_backward (the bound of
+tests/test_gpu_prefill_bwd.py).
 lm_head + argmax: the ids rule of tests/test_gpu_lm_head.py (one ulp of slack
 at a rounding boundary, at most one such row).
 """
@@ -24,7 +29,10 @@ from helpers import ATOL, assert_close, assert_lse_close
 from oracle.attention import causal_attention
 from oracle.decode import paged_decode
 from test_gpu_decode import _paged_case
+from test_gpu_decode_step import _case as _step_case, _check as _check_step
+from test_gpu_decode_step import _fused as _step_fused, _unfused as _step_unfused
 from test_gpu_lm_head import _check as _check_lm_head
+from test_gpu_prefill_bwd import _check as _check_bwd, _inputs as _bwd_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -64,6 +72,35 @@ def _prefill_case(i):
     return dict(B=B, Hq=Hkv * G, Hkv=Hkv, Sq=Sq, off=off, D=D, dtype=dtype)
 
 
+def _step_case_params(i):
+    r = np.random.default_rng(4000 + i)
+    dtype = torch.float16 if r.random() < 0.3 else torch.bfloat16
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    G = int(r.choice([1, 2, 4, 5, 8, 20]))
+    D = int(r.choice([64, 96, 128, 128, 256]))
+    P = int(r.choice([32, 64, 128]))
+    maxp = int(r.integers(1, 21))
+    B = int(r.integers(1, 49))
+    cap = maxp * P
+    lens = r.integers(0, cap + 1, B)
+    if B > 3:  # one past the capacity (dropped), one at the last slot, one empty
+        lens[:3] = [cap + int(r.integers(0, 100)), cap - 1, 0]
+    return dict(lens=[int(x) for x in lens], Hq=Hkv * G, Hkv=Hkv, D=D, P=P, maxp=maxp,
+                dtype=dtype)
+
+
+def _bwd_case(i):
+    r = np.random.default_rng(5000 + i)
+    dtype = torch.float16 if r.random() < 0.3 else torch.bfloat16
+    Hkv = int(r.choice([1, 2, 4]))
+    G = int(r.choice([1, 2, 4]))
+    D = int(r.choice([64, 128]))
+    B = int(r.integers(1, 3))
+    Sq = int(r.integers(1, 300))
+    off = 0 if r.random() < 0.5 else int(r.integers(1, 200))
+    return dict(B=B, Hq=Hkv * G, Hkv=Hkv, Sq=Sq, off=off, D=D, dtype=dtype)
+
+
 def _lm_head_case(i):
     r = np.random.default_rng(3000 + i)
     dtype = torch.float16 if r.random() < 0.3 else torch.bfloat16
@@ -83,6 +120,8 @@ def _id(case):
 DECODE = [_decode_case(i) for i in range(24)]
 PREFILL = [_prefill_case(i) for i in range(16)]
 LM_HEAD = [_lm_head_case(i) for i in range(16)]
+STEP = [_step_case_params(i) for i in range(12)]
+BWD = [_bwd_case(i) for i in range(10)]
 
 
 @pytest.mark.parametrize("case", DECODE, ids=[_id(c) for c in DECODE])
@@ -127,3 +166,19 @@ def test_fuzz_lm_head_argmax(cuda, case):
     hidden = torch.randn(c["B"], c["K"], generator=g).to(c["dtype"]).to(cuda)
     weight = (torch.randn(c["V"], c["K"], generator=g) * 0.02).to(c["dtype"]).to(cuda)
     _check_lm_head(hidden, weight, max_mismatch=1)
+
+
+@pytest.mark.parametrize("case", STEP, ids=[_id(c) for c in STEP])
+def test_fuzz_decode_step(cuda, case):
+    c = case
+    args = _step_case(c["lens"], c["Hq"], c["Hkv"], c["D"], c["P"], c["maxp"], c["dtype"], cuda,
+                      seed=len(c["lens"]) + c["D"])
+    _check_step(_step_fused(*args), _step_unfused(*args), c["dtype"], f"step {_id(c)}")
+
+
+@pytest.mark.parametrize("case", BWD, ids=[_id(c) for c in BWD])
+def test_fuzz_prefill_backward(cuda, case):
+    c = case
+    q, k, v, do = _bwd_inputs(c["B"], c["Hq"], c["Hkv"], c["Sq"], c["Sq"] + c["off"], c["D"],
+                              c["dtype"], cuda, seed=c["Sq"] * 7 + c["off"])
+    _check_bwd(q, k, v, do, c["off"], c["dtype"])
