@@ -407,13 +407,14 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
         for (int r = 0; r < 16; ++r) snx[kt][r] = fmaf(snx[kt][r], a.scale_log2, btile.log2_at(kt, r));
     }
     if constexpr (decltype(mask_c)::value) {
+      // Key k0 + c + 4hh (c the element's compile-time offset) is visible
+      // while k0 + c + 4hh <= qi + q_offset and < Skv, i.e. c < key_lim.
+      const int key_lim = min(qi + a.q_offset + 1, a.Skv) - k0 - hh * 4;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-          if (key > qi + a.q_offset || key >= a.Skv) snx[kt][r] = -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          if (kt * 32 + (r >> 2) * 8 + (r & 3) >= key_lim) snx[kt][r] = -INFINITY;
     }
     // Without a bias raw scores are maxed and the scale (> 0) is applied with
     // the shift; with one they are already in the exp2 domain.
@@ -469,13 +470,14 @@ prefill_mfma_kernel(PrefillArgs a, int hw, int n_rbg) {
   // tile's p recomputed) before the tile's PV.
   auto sm1l = [&](int k0, auto mask_c) __attribute__((always_inline)) {
     if constexpr (decltype(mask_c)::value) {
+      // Key k0 + c + 4hh (c the element's compile-time offset) is visible
+      // while k0 + c + 4hh <= qi + q_offset and < Skv, i.e. c < key_lim.
+      const int key_lim = min(qi + a.q_offset + 1, a.Skv) - k0 - hh * 4;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-          if (key > qi + a.q_offset || key >= a.Skv) snx[kt][r] = -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          if (kt * 32 + (r >> 2) * 8 + (r & 3) >= key_lim) snx[kt][r] = -INFINITY;
     }
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
