@@ -552,6 +552,9 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
       }
     v8 dsop[2][2];
     const int k0 = t * kBwTile;
+    // Key k0 + c + 4hh (c the element's compile-time offset) is visible while
+    // it is <= qi + q_offset and < Skv, i.e. c < key_lim.
+    const int key_lim = min(qi + a.q_offset + 1, a.Skv) - k0 - hh * 4;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -559,8 +562,7 @@ attn_bwd_dq_mfma_kernel(BwdArgs a, int hw, int n_rbg) {
         float x = fmaf(sa[kt][r], a.scale_log2, -lse2);
         if constexpr (BIAS != 0) x += btile.log2_at(kt, r);
         if constexpr (decltype(mask_c)::value) {
-          const int key = k0 + kt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-          if (key > qi + a.q_offset || key >= a.Skv) x = -INFINITY;
+          if (kt * 32 + (r >> 2) * 8 + (r & 3) >= key_lim) x = -INFINITY;
         }
         const float p = lc_exp2(x);
         dsop[kt][r >> 3][r & 7] = static_cast<T>(p * (dpa[kt][r] - dl));
@@ -841,7 +843,9 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a) {
             float x = fmaf(sa[h2][r], a.scale_log2, -l4[i]);
             x += lc_bias_log2(bv[h2][r]);
             if constexpr (decltype(mask_c)::value) {
-              if (kj > qt * kBwTile + row + i + a.q_offset) x = -INFINITY;
+              // kj > qt * kBwTile + row + i + q_offset, with the lane's part
+              // of the row moved to the left: one compare with a constant.
+              if (h2 * 32 + j * 8 + i < kj - qt * kBwTile - hh * 4 - a.q_offset) x = -INFINITY;
             }
             const float p = lc_exp2(x);
             pop[h2][r >> 3][r & 7] = static_cast<T>(p);
@@ -926,7 +930,9 @@ attn_bwd_dkv_mfma_kernel(BwdArgs a) {
         const int row = h2 * 32 + j * 8 + hh * 4;
         float x = fmaf(acc_s[h2][r], a.scale_log2, -l4[h2][j][i]);
         if constexpr (decltype(mask_c)::value) {
-          if (kj > qt * kBwTile + row + i + a.q_offset) x = -INFINITY;
+          // kj > qt * kBwTile + row + i + q_offset, with the lane's part of
+          // the row moved to the left: one compare with a constant.
+          if (h2 * 32 + j * 8 + i < kj - qt * kBwTile - hh * 4 - a.q_offset) x = -INFINITY;
         }
         const float p = lc_exp2(x);
         pop[h2][r >> 3][r & 7] = static_cast<T>(p);
