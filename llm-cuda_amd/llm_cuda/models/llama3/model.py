@@ -168,8 +168,21 @@ class Llama3ForCausalLM(nn.Module):
         max_new_tokens: int = 16,
         use_paged_kv: bool = False,
         page_size: int = 64,
+        use_graph: bool = False,
     ) -> torch.Tensor:
-        """Greedy decoding; returns prompt + max_new_tokens ids."""
+        """Greedy decoding; returns prompt + max_new_tokens ids.
+
+        use_graph (an extension, default off; needs use_paged_kv): the prompt
+        and the first decode step run eagerly, the next decode step is
+        captured in a HIP graph and every later token replays it. The captured
+        kernels take the positions from the cache's device-side lengths, which
+        each replay advances, so the replays give the eager loop's ids; the
+        launch cost of a step (a few hundred kernels at the 8B shape) is paid
+        once instead of per token.
+        """
+        if use_graph and not use_paged_kv:
+            raise ValueError("use_graph needs use_paged_kv=True (the tuple cache grows by "
+                             "concatenation, which a captured graph cannot replay)")
         self.eval()
         generated = input_ids
         if use_paged_kv:
@@ -186,10 +199,29 @@ class Llama3ForCausalLM(nn.Module):
         else:
             past_key_values = None
         cur_input = input_ids
-        for _ in range(max_new_tokens):
+        eager_steps = min(max_new_tokens, 2) if use_graph else max_new_tokens
+        for _ in range(eager_steps):
             next_token, past_key_values = self.greedy_next_token(cur_input, past_key_values)
             generated = torch.cat([generated, next_token], dim=1)
             cur_input = next_token
+        if eager_steps == max_new_tokens:
+            return generated
+        # The eager decode step above allocated what the step needs (counters,
+        # workspaces, tables), so the capture records kernels only. Capturing
+        # runs no kernel: the host-side lengths advance once here while the
+        # device-side ones advance with every replay.
+        static_in = cur_input.clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_out, _ = self.greedy_next_token(static_in, past_key_values)
+        for _ in range(max_new_tokens - eager_steps):
+            graph.replay()
+            next_token = static_out.clone()
+            generated = torch.cat([generated, next_token], dim=1)
+            static_in.copy_(next_token)
+        final = input_ids.shape[1] + max_new_tokens - 1
+        for layer in past_key_values.layer_caches:
+            layer.lengths = [final] * layer.batch_size
         return generated
 
     @torch.no_grad()

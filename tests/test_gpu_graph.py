@@ -118,3 +118,33 @@ def test_ragged_decode_graph_replays_with_ticket(cuda, eager_first):
             assert int(_ops._COUNTERS[key].abs().sum()) == 0
         out, lse = run()  # eager work between replays
         assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype,batch,kv_heads,new", [
+    (torch.float32, 2, 2, 5),     # fp32 (config 1's dtype): RoPE + append, then split-K decode
+    (torch.bfloat16, 32, 8, 6),   # 256 (sequence, kv head) units: the fused decode step
+    (torch.bfloat16, 3, 4, 7),    # split-K decode in bf16
+    (torch.bfloat16, 3, 4, 2),    # two eager steps, nothing to replay
+    (torch.bfloat16, 3, 4, 1),
+])
+def test_generate_with_graph_equals_eager(cuda, dtype, batch, kv_heads, new):
+    """generate(use_graph=True): the prompt and the first decode step eager,
+    the rest replays of one captured step that reads its positions from the
+    cache's device-side lengths. The ids equal the eager loop's (the same
+    kernels on the same inputs), and use_graph without the paged cache raises."""
+    from llm_cuda.models.llama3.config import Llama3Config
+    from llm_cuda.models.llama3.model import Llama3ForCausalLM
+
+    torch.manual_seed(11)
+    cfg = Llama3Config(vocab_size=2000, hidden_size=512, intermediate_size=1024,
+                       num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=kv_heads,
+                       max_position_embeddings=512)
+    model = Llama3ForCausalLM(cfg).to(device=cuda, dtype=dtype).eval()
+    ids = torch.randint(0, cfg.vocab_size, (batch, 9), device=cuda)
+    eager = model.generate(ids, max_new_tokens=new, use_paged_kv=True)
+    graphed = model.generate(ids, max_new_tokens=new, use_paged_kv=True, use_graph=True)
+    torch.cuda.synchronize()
+    assert graphed.shape == (batch, 9 + new)
+    assert torch.equal(graphed, eager)
+    with pytest.raises(ValueError):
+        model.generate(ids, max_new_tokens=2, use_graph=True)
