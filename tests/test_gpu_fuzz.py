@@ -20,14 +20,19 @@ oracle.attention.causal_attention_backward (the bound of
 tests/test_gpu_prefill_bwd.py).
 lm_head + argmax: the ids rule of tests/test_gpu_lm_head.py (one ulp of slack
 at a rounding boundary, at most one such row).
+Elementwise (RMSNorm, add + RMSNorm, SwiGLU, RoPE): random widths (odd ones
+take the element-wise path), rows taken from wider buffers at random offsets
+(strided, possibly unaligned), fp32/f16/bf16, against oracle.elementwise with
+the bounds of tests/test_gpu_elementwise.py; the residual sum bit-exact.
 """
 import numpy as np
 import pytest
 import torch
 
-from helpers import ATOL, assert_close, assert_lse_close
+from helpers import ATOL, RTOL, assert_close, assert_lse_close
 from oracle.attention import causal_attention
 from oracle.decode import paged_decode
+from oracle.elementwise import apply_rope, rms_norm, swiglu
 from test_gpu_decode import _paged_case
 from test_gpu_decode_step import _case as _step_case, _check as _check_step
 from test_gpu_decode_step import _fused as _step_fused, _unfused as _step_unfused
@@ -111,16 +116,31 @@ def _lm_head_case(i):
     return dict(B=B, K=K, V=V, dtype=dtype)
 
 
+def _ew_case(i):
+    r = np.random.default_rng(6000 + i)
+    dtype = [torch.float32, torch.float16, torch.bfloat16][int(r.integers(0, 3))]
+    kind = ["rmsnorm", "add_rmsnorm", "swiglu", "rope"][i % 4]
+    rows = int(r.integers(1, 40))
+    width = int(r.choice([16, 100, 256, 1001, 4096, 5000, 14336, 20480]))
+    if kind == "rope":
+        width = int(r.choice([16, 32, 64, 96, 128, 256]))  # head_dim
+    pad = int(r.choice([0, 0, 8, 3]))  # row stride width + pad, rows start at offset pad
+    return dict(kind=kind, rows=rows, width=width, pad=pad, dtype=dtype)
+
+
+_DT = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+
 def _id(case):
     return "-".join(f"{k}{v}" if k != "lens" else f"B{len(v)}max{max(v)}"
-                    for k, v in case.items() if k != "dtype") + \
-        ("-f16" if case["dtype"] == torch.float16 else "-bf16")
+                    for k, v in case.items() if k != "dtype") + "-" + _DT[case["dtype"]]
 
 
 DECODE = [_decode_case(i) for i in range(24)]
 PREFILL = [_prefill_case(i) for i in range(16)]
 LM_HEAD = [_lm_head_case(i) for i in range(16)]
 STEP = [_step_case_params(i) for i in range(12)]
+ELEMENTWISE = [_ew_case(i) for i in range(24)]
 BWD = [_bwd_case(i) for i in range(10)]
 
 
@@ -182,3 +202,44 @@ def test_fuzz_prefill_backward(cuda, case):
     q, k, v, do = _bwd_inputs(c["B"], c["Hq"], c["Hkv"], c["Sq"], c["Sq"] + c["off"], c["D"],
                               c["dtype"], cuda, seed=c["Sq"] * 7 + c["off"])
     _check_bwd(q, k, v, do, c["off"], c["dtype"])
+
+
+@pytest.mark.parametrize("case", ELEMENTWISE, ids=[_id(c) for c in ELEMENTWISE])
+def test_fuzz_elementwise(cuda, case):
+    from llm_cuda.kernels import _ops
+
+    c = case
+    dt, rows, n, pad = c["dtype"], c["rows"], c["width"], c["pad"]
+    g = torch.Generator().manual_seed(rows * 131 + n + pad)
+    tol, rtol = ATOL[dt], RTOL[dt]
+
+    def strided(cols):  # rows x cols inside a [rows, cols + pad] buffer, from column pad
+        base = torch.randn(rows, cols + 2 * pad, generator=g).to(dt).to(cuda)
+        return base[:, pad:pad + cols]
+
+    if c["kind"] in ("rmsnorm", "add_rmsnorm"):
+        x, w = strided(n), (1 + 0.1 * torch.randn(n, generator=g)).to(dt).to(cuda)
+        if c["kind"] == "rmsnorm":
+            y = _ops.rms_norm(x, w, 1e-5)
+            ref = rms_norm(x.cpu(), w.cpu(), 1e-5)
+        else:
+            res = strided(n)
+            y, ssum = _ops.add_rms_norm(x, res, w, 1e-5)
+            assert torch.equal(ssum, x + res), "residual sum"
+            ref = rms_norm((x + res).cpu(), w.cpu(), 1e-5)
+        assert_close(y, ref, tol, _id(c), rtol=rtol)
+    elif c["kind"] == "swiglu":
+        gate, up = strided(n), strided(n)
+        gate.mul_(3)  # in place: the view keeps its strides
+        assert_close(_ops.swiglu(gate, up), swiglu(gate.cpu(), up.cpu()), tol, _id(c), rtol=rtol)
+    else:
+        from llm_cuda.kernels.triton.rope import triton_apply_rope
+
+        D, H, S = n, 1 + rows % 5, 1 + rows
+        q = torch.randn(2, S, H * D + pad, generator=g).to(dt).to(cuda)[..., :H * D]
+        q = q.view(2, S, H, D).transpose(1, 2)  # projection-view strides
+        cos = torch.randn(S, D, generator=g).to(dt).to(cuda)  # full-width tables, unequal halves
+        sin = torch.randn(S, D, generator=g).to(dt).to(cuda)
+        out = triton_apply_rope(q, cos, sin)
+        ref = apply_rope(q.cpu(), cos.cpu(), sin.cpu())
+        assert_close(out, ref, tol, _id(c), rtol=rtol)
