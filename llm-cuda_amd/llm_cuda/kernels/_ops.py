@@ -765,6 +765,8 @@ def choose_split_tokens(batch: int, n_kv_heads: int, group: int, capacity_tokens
     one-wave splits: 512 tokens, shrunk until there are >= 1024 of them.
     """
     units = batch * n_kv_heads * ((group + 15) // 16)
+    if units == 0:  # an empty batch launches nothing; any valid split will do
+        return max(64, -(-capacity_tokens // 64) * 64)
     if page_size % 32 == 0 and capacity_tokens > 0:
         if uniform_length is not None:
             length = max(1, min(int(uniform_length), capacity_tokens))
@@ -862,6 +864,9 @@ def _paged_decode(q: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.T
         block_table = block_table.contiguous()
     if not seq_lens.is_contiguous():
         seq_lens = seq_lens.contiguous()
+    if B == 0:
+        out = torch.empty_like(q)
+        return (out, torch.empty(0, Hq, dtype=torch.float32, device=dev)) if return_lse else out
     maxp = block_table.shape[1]
     capacity = maxp * P
     G = Hq // Hkv

@@ -244,6 +244,9 @@ def test_split_heuristic():
     # equal lengths: the fewest splits per unit that fill rounds of the CUs
     assert choose_split_tokens(64, 8, 4, 4160, 64, 128, 4096) == 4160  # 512 units, 1 split
     assert choose_split_tokens(48, 8, 4, 8192, 64, 128, 8000) == 4032  # 384 units, 2 splits
+    # an empty batch launches nothing: any multiple of 64 covering the capacity
+    assert choose_split_tokens(0, 8, 4, 8000) == 8000
+    assert choose_split_tokens(0, 8, 4, 8000, 64, 128, 100) == 8000
     # pages of 48 tokens: one-wave splits only
     assert choose_split_tokens(64, 8, 4, 8000, 48) == 512
     assert choose_split_tokens(1, 2, 4, 128, 48) == 64
